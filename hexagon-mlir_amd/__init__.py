@@ -1,0 +1,47 @@
+"""hexagon_mlir_amd — MI355X-native replacement of Hexagon-MLIR's matmul / GEMV /
+RMSNorm / softmax hot path.
+
+Layers:
+  * ``csrc/``      hand-written HIP kernels for gfx950 behind the C ABI of
+                   ``include/hxmi.h`` (built into ``lib/libhxmi.so``);
+  * ``hxmi``       ctypes binding and torch-tensor ops over that ABI;
+  * ``backend``    the reference's Python surface (``HexagonOptions``,
+                   ``TorchMLIRHexagonLauncher.run_torch_mlir``) on top of it.
+
+The directory name carries a dash, so it is imported under the module name
+``hexagon_mlir_amd`` (see ``load_package`` in the repository's
+``__graft_entry__.py``).
+"""
+from . import hxmi
+from .hxmi import (
+    HxmiError,
+    HxmiNotBuiltError,
+    attention,
+    bgemm,
+    gemm,
+    gemv,
+    hexkl_matmul,
+    linear,
+    load_library,
+    pack_gate_up,
+    rms_norm,
+    softmax,
+    w8a16_linear,
+)
+
+__all__ = [
+    "hxmi",
+    "HxmiError",
+    "HxmiNotBuiltError",
+    "attention",
+    "bgemm",
+    "gemm",
+    "gemv",
+    "hexkl_matmul",
+    "linear",
+    "load_library",
+    "pack_gate_up",
+    "rms_norm",
+    "softmax",
+    "w8a16_linear",
+]

@@ -1,0 +1,225 @@
+// extern "C" entry points declared in include/hxmi.h: argument validation,
+// error reporting, dispatch to the kernel launchers.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/hxmi.h"
+#include "hxmi_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return HXMI_OK;
+}
+
+int from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  if (e == hipErrorNotSupported) return fail(HXMI_ERR_UNSUPPORTED, "%s: unsupported shape/alignment", what);
+  return fail(HXMI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define REQUIRE(cond, ...)                                   \
+  do {                                                       \
+    if (!(cond)) return fail(HXMI_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M,
+                int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC,
+                int b_is_nt, int epilogue, float alpha, int out_f32, void* stream, const char* name) {
+  REQUIRE(batch >= 0 && M >= 0 && N >= 0 && K >= 0, "%s: negative size (batch=%lld M=%lld N=%lld K=%lld)", name,
+          (long long)batch, (long long)M, (long long)N, (long long)K);
+  REQUIRE(b_is_nt == 0 || b_is_nt == 1, "%s: b_is_nt must be 0 or 1", name);
+  REQUIRE(epilogue >= HXMI_EPI_NONE && epilogue <= HXMI_EPI_BIAS_GELU_TANH, "%s: unknown epilogue %d", name,
+          epilogue);
+  const int64_t nout = epilogue == HXMI_EPI_SILU_MUL ? N / 2 : N;
+  if (batch == 0 || M == 0 || nout == 0) return ok();
+  REQUIRE(epilogue != HXMI_EPI_SILU_MUL || N % 32 == 0, "%s: SiLU-mul needs N %% 32 == 0 (packed gate/up), got %lld",
+          name, (long long)N);
+  REQUIRE(A && B && C, "%s: null operand pointer", name);
+  REQUIRE(bias || (epilogue != HXMI_EPI_BIAS && epilogue != HXMI_EPI_BIAS_GELU_TANH),
+          "%s: epilogue %d needs a bias pointer", name, epilogue);
+  REQUIRE(lda >= K && ldb >= (b_is_nt ? K : N) && ldc >= nout, "%s: leading dimension too small (lda=%lld ldb=%lld ldc=%lld)",
+          name, (long long)lda, (long long)ldb, (long long)ldc);
+  REQUIRE(sA >= 0 && sB >= 0 && sC >= 0, "%s: negative batch stride", name);
+  hxmi::GemmProblem p{};
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.bias = bias;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.ldc = ldc;
+  p.sA = sA;
+  p.sB = sB;
+  p.sC = sC;
+  p.batch = batch;
+  p.alpha = alpha;
+  p.dtype = dtype;
+  p.b_nt = b_is_nt;
+  p.epilogue = epilogue;
+  p.out_f32 = out_f32;
+  p.tile = -1;
+  return from_hip(hxmi::launch_gemm(p, (hipStream_t)stream), name);
+}
+
+int row_common(bool rms, int dtype, const void* x, const void* g, void* y, int64_t rows, int64_t cols, int64_t ldx,
+               int64_t ldy, float eps, float scale, void* stream, const char* name) {
+  REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", name);
+  if (rows == 0 || cols == 0) return ok();
+  REQUIRE(x && y && (g || !rms), "%s: null pointer", name);
+  REQUIRE(ldx >= cols && ldy >= cols, "%s: leading dimension smaller than cols", name);
+  REQUIRE(cols < (1ll << 31), "%s: cols too large", name);
+  hxmi::RowProblem p{};
+  p.x = x;
+  p.g = g;
+  p.y = y;
+  p.rows = rows;
+  p.cols = cols;
+  p.ldx = ldx;
+  p.ldy = ldy;
+  p.eps = eps;
+  p.scale = scale;
+  p.dtype = dtype;
+  return from_hip(rms ? hxmi::launch_rmsnorm(p, (hipStream_t)stream) : hxmi::launch_softmax(p, (hipStream_t)stream),
+                  name);
+}
+
+bool al(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* hxmi_last_error(void) { return g_err; }
+
+int hxmi_version(void) { return 100; }
+
+int hxmi_gemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                  int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream) {
+  return gemm_common(hxmi::DT_F16, A, B, C, bias, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, b_is_nt, epilogue, alpha, 0,
+                     stream, "hxmi_gemm_f16");
+}
+
+int hxmi_gemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream) {
+  return gemm_common(hxmi::DT_BF16, A, B, C, bias, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, b_is_nt, epilogue, alpha, 0,
+                     stream, "hxmi_gemm_bf16");
+}
+
+int hxmi_bgemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M, int64_t N,
+                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
+                   int64_t strideC, int b_is_nt, int epilogue, float alpha, void* stream) {
+  return gemm_common(hxmi::DT_F16, A, B, C, bias, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, b_is_nt,
+                     epilogue, alpha, 0, stream, "hxmi_bgemm_f16");
+}
+
+int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M, int64_t N,
+                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
+                    int64_t strideC, int b_is_nt, int epilogue, float alpha, void* stream) {
+  return gemm_common(hxmi::DT_BF16, A, B, C, bias, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, b_is_nt,
+                     epilogue, alpha, 0, stream, "hxmi_bgemm_bf16");
+}
+
+int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                  int64_t ldx, int64_t ldw, int64_t ldy, void* stream) {
+  const char* name = "hxmi_gemv_f16";
+  REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", name);
+  if (M == 0 || N == 0) return ok();
+  REQUIRE(x && W && y, "%s: null pointer", name);
+  REQUIRE(ldx >= K && ldw >= K && ldy >= N, "%s: leading dimension too small", name);
+  const bool gemv_ok = M <= 16 && K % 8 == 0 && N % 4 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldy % 4 == 0 &&
+                       al(x, 16) && al(W, 16) && al(y, 8) && (!bias || al(bias, 8)) && 64 * ldw * 2 < (1ll << 31) &&
+                       16 * ldx * 2 < (1ll << 31);
+  if (!gemv_ok)
+    return gemm_common(hxmi::DT_F16, x, W, y, bias, 1, M, N, K, ldx, ldw, ldy, 0, 0, 0, 1,
+                       bias ? HXMI_EPI_BIAS : HXMI_EPI_NONE, 1.f, 0, stream, name);
+  hxmi::GemvProblem p{};
+  p.x = x;
+  p.W = W;
+  p.bias = bias;
+  p.y = y;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldy = ldy;
+  p.w_int8 = 0;
+  return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
+}
+
+int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const void* bias, void* y, int64_t M,
+                    int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* stream) {
+  const char* name = "hxmi_gemv_w8a16";
+  REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", name);
+  if (M == 0 || N == 0) return ok();
+  REQUIRE(x && Wq && scale && y, "%s: null pointer", name);
+  REQUIRE(ldx >= K && ldw >= K && ldy >= N, "%s: leading dimension too small", name);
+  REQUIRE(K % 16 == 0 && ldw % 16 == 0 && N % 4 == 0 && ldx % 8 == 0 && ldy % 8 == 0,
+          "%s: needs K %% 16 == 0, ldw %% 16 == 0, N %% 4 == 0, ldx %% 8 == 0, ldy %% 8 == 0", name);
+  REQUIRE(al(x, 16) && al(Wq, 16) && al(y, 16) && al(scale, 8) && (!bias || al(bias, 8)),
+          "%s: x, Wq, y need 16-byte and scale/bias 8-byte alignment", name);
+  REQUIRE(256 * ldw < (1ll << 31) && 256 * ldx * 2 < (1ll << 31), "%s: leading dimension too large", name);
+  hxmi::GemvProblem p{};
+  p.x = x;
+  p.W = Wq;
+  p.scale = scale;
+  p.bias = bias;
+  p.y = y;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldy = ldy;
+  p.w_int8 = 1;
+  if (M <= 16) return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
+  REQUIRE(N % 8 == 0, "%s: M > 16 needs N %% 8 == 0", name);
+  return from_hip(hxmi::launch_w8a16_gemm(p, (hipStream_t)stream), name);
+}
+
+int hxmi_rmsnorm_f16(const void* x, const void* g, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy,
+                     float eps, void* stream) {
+  return row_common(true, hxmi::DT_F16, x, g, y, rows, cols, ldx, ldy, eps, 1.f, stream, "hxmi_rmsnorm_f16");
+}
+
+int hxmi_rmsnorm_bf16(const void* x, const void* g, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy,
+                      float eps, void* stream) {
+  return row_common(true, hxmi::DT_BF16, x, g, y, rows, cols, ldx, ldy, eps, 1.f, stream, "hxmi_rmsnorm_bf16");
+}
+
+int hxmi_softmax_f16(const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float scale,
+                     void* stream) {
+  return row_common(false, hxmi::DT_F16, x, nullptr, y, rows, cols, ldx, ldy, 0.f, scale, stream, "hxmi_softmax_f16");
+}
+
+int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float scale,
+                      void* stream) {
+  return row_common(false, hxmi::DT_BF16, x, nullptr, y, rows, cols, ldx, ldy, 0.f, scale, stream,
+                    "hxmi_softmax_bf16");
+}
+
+int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,
+                            const hxmi_f16_t* inW) {
+  const int rc = gemm_common(hxmi::DT_F16, inAct, inW, outM, nullptr, 1, n_row, n_col, n_inner, n_inner, n_col, n_col,
+                             0, 0, 0, 0, HXMI_EPI_NONE, 1.f, 1, nullptr, "hexkl_matmul_f16f16_f32");
+  if (rc != HXMI_OK) return rc;
+  return from_hip(hipStreamSynchronize(nullptr), "hexkl_matmul_f16f16_f32");
+}
+
+}  // extern "C"

@@ -1,0 +1,31 @@
+// Instantiations of the MFMA GEMM for f16 operands.
+#include "gemm_impl.h"
+
+namespace hxmi {
+namespace gemm {
+
+hipError_t launch_fast_f16(int tile, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s) {
+  using T = _Float16;
+  if (out_f32) {
+    if (epi != EPI_NONE) return hipErrorNotSupported;
+    return nn ? launch_tile<true, T, EPI_NONE, true>(tile, k, s) : launch_tile<false, T, EPI_NONE, true>(tile, k, s);
+  }
+  if (nn) {
+    switch (epi) {
+      case EPI_NONE: return launch_tile<true, T, EPI_NONE, false>(tile, k, s);
+      case EPI_BIAS: return launch_tile<true, T, EPI_BIAS, false>(tile, k, s);
+      default: return hipErrorNotSupported;
+    }
+  }
+  switch (epi) {
+    case EPI_NONE: return launch_tile<false, T, EPI_NONE, false>(tile, k, s);
+    case EPI_BIAS: return launch_tile<false, T, EPI_BIAS, false>(tile, k, s);
+    case EPI_SILU_MUL: return launch_tile<false, T, EPI_SILU_MUL, false>(tile, k, s);
+    case EPI_GELU_TANH: return launch_tile<false, T, EPI_GELU_TANH, false>(tile, k, s);
+    case EPI_BIAS_GELU_TANH: return launch_tile<false, T, EPI_BIAS_GELU_TANH, false>(tile, k, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+}  // namespace gemm
+}  // namespace hxmi

@@ -1,0 +1,206 @@
+// Decode-shaped y[M,N] = x[M,K] . W[N,K]^T (+bias) for M <= 16, HBM-bound.
+//
+// The reference has no dedicated GEMV: M = 1 matmuls go through its generic
+// HVX matmul schedule (ScheduleMatmulForHVXPass.cpp:69-195, TilingPass.cpp
+// :108-251).  Here W is streamed from HBM exactly once:
+//   * a workgroup owns TPB tiles of 16 weight rows; its KS waves split K into
+//     contiguous ranges so each wave streams long runs of every row;
+//   * each lane loads 16 contiguous bytes of a row per step (16 rows x 64 B
+//     per wave instruction) straight into the A operand of
+//     v_mfma_f32_16x16x32_f16; x (M <= 16 rows, zero-padded by out-of-range
+//     buffer loads) is the B operand, so M = 1..16 cost the same HBM bytes;
+//   * int8 weights (weight-only quantisation) are converted to fp16 in
+//     registers (exact for q in [-128,127]); the per-row scale multiplies the
+//     fp32 sum once, after the K reduction;
+//   * partial sums of the KS waves are reduced through LDS.
+#include "hxmi_common.h"
+#include "hxmi_internal.h"
+
+namespace hxmi {
+namespace {
+
+struct VArgs {
+  const char* x;
+  const char* W;
+  const char* scale;
+  const char* bias;
+  char* y;
+  int M, N, K;
+  int64_t ldx, ldw, ldy;
+};
+
+__device__ __forceinline__ float4v mfma16(short8v a, short8v b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a), __builtin_bit_cast(half8v, b),
+                                                c, 0, 0, 0);
+}
+
+// 8 int8 weights -> 8 exact fp16 (see the GEMM's dequant8 for the method).
+__device__ __forceinline__ short8v dequant8v(uint32_t d0, uint32_t d1) {
+  short8v out;
+  half2v* o = (half2v*)&out;
+  const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const uint32_t u0 = d0 ^ 0x80808080u, u1 = d1 ^ 0x80808080u;
+  o[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) - bias;
+  o[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) - bias;
+  o[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) - bias;
+  o[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) - bias;
+  return out;
+}
+
+template <int TPB, int KS, bool I8, int UNR>
+__global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
+  // k covered by one lane-load step: fp16 -> 32 (one MFMA), int8 -> 64 (two)
+  constexpr int KSTEP = I8 ? 64 : 32;
+  __shared__ float4v red[KS][TPB][64];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * (TPB * 16);
+  const int nsteps = (a.K + KSTEP - 1) / KSTEP;
+  const int per_wave = (nsteps + KS - 1) / KS;
+  const int s_begin = w * per_wave;
+  const int s_end = min(nsteps, s_begin + per_wave);
+
+  const int r16 = lane & 15, kq = lane >> 4;  // row within tile, k quarter
+  const int esz = I8 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
+  const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
+  bool rowok[TPB];
+  uint32_t wbase[TPB];
+#pragma unroll
+  for (int t = 0; t < TPB; ++t) {
+    rowok[t] = (n0 + t * 16 + r16) < a.N;
+    wbase[t] = (uint32_t)((t * 16 + r16) * a.ldw * esz);
+  }
+  const bool mok = r16 < a.M;
+  const uint32_t xbase = (uint32_t)(r16 * a.ldx * 2);
+
+  float4v acc[TPB];
+#pragma unroll
+  for (int t = 0; t < TPB; ++t) acc[t] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  for (int s0 = s_begin; s0 < s_end; s0 += UNR) {
+    int4v wv[UNR][TPB];
+    int4v xv[UNR][I8 ? 2 : 1];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int s = s0 + u;
+      const bool sok = s < s_end;
+      if constexpr (I8) {
+        const int k = s * 64 + kq * 16;  // 16 int8 weights per lane
+        const bool kok = sok && k < a.K;
+#pragma unroll
+        for (int t = 0; t < TPB; ++t) wv[u][t] = load16(rW, (kok && rowok[t]) ? wbase[t] + k : kOOB);
+        xv[u][0] = load16(rX, (kok && mok) ? xbase + k * 2 : kOOB);
+        xv[u][1] = load16(rX, (kok && mok) ? xbase + k * 2 + 16 : kOOB);
+      } else {
+        const int k = s * 32 + kq * 8;
+        const bool kok = sok && k < a.K;
+#pragma unroll
+        for (int t = 0; t < TPB; ++t) wv[u][t] = load16(rW, (kok && rowok[t]) ? wbase[t] + k * 2 : kOOB);
+        xv[u][0] = load16(rX, (kok && mok) ? xbase + k * 2 : kOOB);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+#pragma unroll
+      for (int t = 0; t < TPB; ++t) {
+        if constexpr (I8) {
+          const short8v w0 = dequant8v((uint32_t)wv[u][t][0], (uint32_t)wv[u][t][1]);
+          const short8v w1 = dequant8v((uint32_t)wv[u][t][2], (uint32_t)wv[u][t][3]);
+          acc[t] = mfma16(w0, __builtin_bit_cast(short8v, xv[u][0]), acc[t]);
+          acc[t] = mfma16(w1, __builtin_bit_cast(short8v, xv[u][1]), acc[t]);
+        } else {
+          acc[t] = mfma16(__builtin_bit_cast(short8v, wv[u][t]), __builtin_bit_cast(short8v, xv[u][0]), acc[t]);
+        }
+      }
+    }
+  }
+
+  if constexpr (KS > 1) {
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) red[w][t][lane] = acc[t];
+    __syncthreads();
+  }
+  // wave w finalises tiles t = w, w + KS, ...
+  for (int t = w; t < TPB; t += KS) {
+    float4v sum = acc[t];
+    if constexpr (KS > 1) {
+      sum = red[0][t][lane];
+#pragma unroll
+      for (int q = 1; q < KS; ++q) sum += red[q][t][lane];
+    }
+    // D[n][m]: lane holds m = lane % 16, n = 4*(lane / 16) + 0..3
+    const int m = lane & 15;
+    const int n = n0 + t * 16 + 4 * (lane >> 4);
+    if (m < a.M && n < a.N) {
+      float v[4] = {sum[0], sum[1], sum[2], sum[3]};
+      if (I8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] *= (float)((const _Float16*)a.scale)[n + q];
+      }
+      if (a.bias) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] += (float)((const _Float16*)a.bias)[n + q];
+      }
+      _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+      *(short4v*)(a.y + ((int64_t)m * a.ldy + n) * 2) = __builtin_bit_cast(short4v, h);
+    }
+  }
+}
+
+template <int TPB, int KS, bool I8>
+hipError_t launch_cfg(const VArgs& v, hipStream_t stream) {
+  constexpr int UNR = TPB >= 4 ? 2 : 4;
+  const int blocks = (v.N + TPB * 16 - 1) / (TPB * 16);
+  hipLaunchKernelGGL((gemv_mfma<TPB, KS, I8, UNR>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+  return hipGetLastError();
+}
+
+template <bool I8>
+hipError_t launch_sel(int tpb, int ks, const VArgs& v, hipStream_t stream) {
+  if (tpb == 4) {
+    if (ks == 4) return launch_cfg<4, 4, I8>(v, stream);
+    if (ks == 8) return launch_cfg<4, 8, I8>(v, stream);
+    return launch_cfg<4, 16, I8>(v, stream);
+  }
+  if (tpb == 2) {
+    if (ks == 4) return launch_cfg<2, 4, I8>(v, stream);
+    if (ks == 8) return launch_cfg<2, 8, I8>(v, stream);
+    return launch_cfg<2, 16, I8>(v, stream);
+  }
+  if (ks == 4) return launch_cfg<1, 4, I8>(v, stream);
+  if (ks == 8) return launch_cfg<1, 8, I8>(v, stream);
+  return launch_cfg<1, 16, I8>(v, stream);
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
+  if (p.M == 0 || p.N == 0) return hipSuccess;
+  VArgs v;
+  v.x = (const char*)p.x;
+  v.W = (const char*)p.W;
+  v.scale = (const char*)p.scale;
+  v.bias = (const char*)p.bias;
+  v.y = (char*)p.y;
+  v.M = (int)p.M;
+  v.N = (int)p.N;
+  v.K = (int)p.K;
+  v.ldx = p.ldx;
+  v.ldw = p.ldw;
+  v.ldy = p.ldy;
+  // Rows per workgroup and K split: aim for >= ~2048 waves in flight so
+  // enough 16-byte loads are outstanding to cover HBM latency.
+  const int64_t tiles16 = (p.N + 15) / 16;
+  int tpb = tiles16 >= 4096 ? 4 : (tiles16 >= 1024 ? 2 : 1);
+  const int64_t blocks = (tiles16 + tpb - 1) / tpb;
+  int ks = 4;
+  while (ks < 16 && blocks * ks < 2048) ks *= 2;
+  const int kstep = p.w_int8 ? 64 : 32;
+  const int64_t nsteps = (p.K + kstep - 1) / kstep;
+  while (ks > 4 && nsteps / ks < 2) ks /= 2;
+  return p.w_int8 ? launch_sel<true>(tpb, ks, v, stream) : launch_sel<false>(tpb, ks, v, stream);
+}
+
+}  // namespace hxmi

@@ -1,0 +1,112 @@
+// Device-side building blocks shared by every hxmi kernel (gfx950 / CDNA4 only).
+//
+// Vector types for MFMA operands, buffer-resource loads with hardware
+// out-of-range zeroing, wave64 reductions, and the small math helpers the
+// fused epilogues and row reductions use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define HXMI_LDS __attribute__((address_space(3)))
+
+typedef _Float16 hx_half;
+typedef __bf16 hx_bf16;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef short short8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef int int2v __attribute__((ext_vector_type(2)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(8)));
+typedef short i16x4_raw __attribute__((__vector_size__(8)));
+
+namespace hxmi {
+
+// Offset that is always beyond a buffer resource's num_records: a lane that
+// loads from it receives zeros instead of touching memory.
+constexpr uint32_t kOOB = 0x80000000u;
+
+// Raw buffer resource for gfx9-family (CDNA) parts: base, no swizzle stride,
+// num_records in bytes, dword3 = data-format word used for untyped loads.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// 16-byte global -> LDS copy that bypasses VGPRs. Lane i of the wave writes
+// lds_wave_base + 16*i; voffset is this lane's byte offset into the buffer.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, HXMI_LDS void* lds_wave_base,
+                                           uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_wave_base, 16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ int4v load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voffset, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+__device__ __forceinline__ HXMI_LDS char* to_lds(char* p) { return (HXMI_LDS char*)(p); }
+
+// ds_read_b64_tr_b16: within each 16-lane group the 4x16 block of b16 values
+// addressed by the lanes (lane L supplies row L/4, columns 4*(L%4)..+3) is
+// returned transposed: lane i receives column i, rows 0..3.
+__device__ __forceinline__ short4v lds_read_tr16(const char* p) {
+  fp16x4_raw v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((HXMI_LDS fp16x4_raw*)(to_lds(const_cast<char*>(p))));
+  return __builtin_bit_cast(short4v, v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = width / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp(float x) {
+  // e^x = 2^(x*log2(e)); v_exp_f32 evaluates 2^x.
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + fast_exp(-x)); }
+
+// tanh-form GELU, 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))), evaluated as
+// x*sigmoid(2u) which equals it exactly in real arithmetic and avoids tanh's
+// cancellation near 0.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  float u = k0 * (x + k1 * x * x * x);
+  return x / (1.0f + fast_exp(-2.0f * u));
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  return (float)v;
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) {
+  return (T)v;
+}
+
+}  // namespace hxmi

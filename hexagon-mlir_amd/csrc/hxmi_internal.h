@@ -1,0 +1,93 @@
+// Host-side launch interface between the C ABI (capi.hip) and the kernel
+// translation units. Nothing here crosses the library boundary.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hxmi {
+
+enum Dtype { DT_F16 = 0, DT_BF16 = 1, DT_W8A16 = 2 /* fp16 A, int8 B */ };
+
+enum Epilogue {
+  EPI_NONE = 0,
+  EPI_BIAS = 1,
+  EPI_SILU_MUL = 2,
+  EPI_GELU_TANH = 3,
+  EPI_BIAS_GELU_TANH = 4,
+};
+
+enum OutType { OUT_SAME = 0, OUT_F32 = 1 };
+
+// One (optionally batched) GEMM  C[b] = epilogue(alpha * A[b] . op(B[b])).
+// A is [M,K] row-major with leading dimension lda.  B is [K,N] (b_nt = 0) or
+// [N,K] (b_nt = 1).  For EPI_SILU_MUL, N counts the packed gate/up columns of
+// B and C receives N/2 columns.
+struct GemmProblem {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* bias;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t sA, sB, sC;  // batch strides, elements
+  int64_t batch;
+  float alpha;
+  int dtype;     // Dtype of A, B and (unless out_f32) C
+  int b_nt;      // 1: B is [N,K]
+  int epilogue;  // Epilogue
+  int out_f32;   // 1: C is fp32
+  int tile;      // forced tile id (< 0: heuristic)
+};
+
+// Tile shapes the fast kernel is instantiated for.
+enum TileId { TILE_256x256 = 0, TILE_128x256, TILE_256x128, TILE_128x128, TILE_64x128, TILE_128x64, TILE_64x64, TILE_COUNT };
+
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream);
+// Whether p satisfies the alignment rules of the MFMA fast path.
+bool gemm_fast_path_ok(const GemmProblem& p);
+int gemm_pick_tile(const GemmProblem& p);
+
+struct GemvProblem {
+  const void* x;      // [M,K] fp16
+  const void* W;      // [N,K] fp16 or int8
+  const void* scale;  // [N] fp16 (int8 weights only)
+  const void* bias;   // [N] fp16 or null
+  void* y;            // [M,N] fp16
+  int64_t M, N, K;
+  int64_t ldx, ldw, ldy;
+  int w_int8;
+};
+
+hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream);
+
+// W8A16 GEMM for larger M (MFMA, int8 weights dequantised in registers).
+hipError_t launch_w8a16_gemm(const GemvProblem& p, hipStream_t stream);
+
+struct RowProblem {
+  const void* x;
+  const void* g;  // RMSNorm weight or null
+  void* y;
+  int64_t rows, cols, ldx, ldy;
+  float eps;    // RMSNorm
+  float scale;  // softmax: y = softmax(scale * x)
+  int dtype;
+};
+
+hipError_t launch_rmsnorm(const RowProblem& p, hipStream_t stream);
+hipError_t launch_softmax(const RowProblem& p, hipStream_t stream);
+
+struct AttnProblem {
+  const void* q;  // [B*H, S, D]
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t bh, s, d;
+  int64_t sq, sk, sv, so;  // per-(b,h) strides, elements
+  int64_t ldq, ldk, ldv, ldo;
+  float scale;
+};
+
+hipError_t launch_attention(const AttnProblem& p, hipStream_t stream);
+
+}  // namespace hxmi

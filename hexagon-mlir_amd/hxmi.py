@@ -1,0 +1,355 @@
+"""ctypes binding of libhxmi.so and the torch-tensor ops built on it.
+
+PyTorch-ROCm supplies device memory and the current HIP stream; every
+computation runs in the hand-written HIP kernels of ``csrc/``.  There is no
+fallback: if the library is missing, or a tensor is not on the GPU, the call
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+from typing import Optional
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "libhxmi.so"
+
+EPILOGUES = {
+    None: 0,
+    "none": 0,
+    "bias": 1,
+    "silu_mul": 2,
+    "gelu_tanh": 3,
+    "bias_gelu_tanh": 4,
+}
+
+# Every symbol include/hxmi.h declares, with its ctypes signature.
+_I64 = ctypes.c_int64
+_P = ctypes.c_void_p
+_F = ctypes.c_float
+_I = ctypes.c_int
+SIGNATURES = {
+    "hxmi_last_error": ([], ctypes.c_char_p),
+    "hxmi_version": ([], _I),
+    "hxmi_gemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
+    "hxmi_gemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
+    "hxmi_bgemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
+    "hxmi_bgemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
+    "hxmi_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_gemv_w8a16": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_rmsnorm_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
+    "hxmi_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
+    "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
+    "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
+    "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
+}
+
+
+class HxmiError(RuntimeError):
+    """A kernel call was rejected or failed."""
+
+
+class HxmiNotBuiltError(HxmiError):
+    """libhxmi.so has not been built (run hexagon-mlir_amd/build.py)."""
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libhxmi.so (once) and bind the signatures of every entry point."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise HxmiNotBuiltError(f"{LIB_PATH} is missing; build it with hexagon-mlir_amd/build.py")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = load_library().hxmi_last_error().decode(errors="replace")
+        raise HxmiError(f"hxmi error {rc}: {msg}")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(*ts: Optional[torch.Tensor]) -> None:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise HxmiError("hxmi ops take GPU tensors; got a tensor on " + str(t.device))
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise HxmiError(f"tensors on different devices: {dev} and {t.device}")
+
+
+def _rowmajor(t: torch.Tensor, name: str) -> int:
+    """Leading dimension of a 2-D view with unit stride in the last dim."""
+    if t.dim() != 2:
+        raise HxmiError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.size(1) > 1:
+        raise HxmiError(f"{name} must have unit stride in its last dimension")
+    return max(t.stride(0), t.size(1), 1)
+
+
+def _vec(t: Optional[torch.Tensor], n: int, dtype: torch.dtype, name: str) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    if t.dtype != dtype or t.dim() != 1 or t.numel() != n:
+        raise HxmiError(f"{name} must be a 1-D {dtype} tensor of {n} elements")
+    return t.contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def gemm(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    *,
+    b_layout: str = "nn",
+    epilogue: Optional[str] = None,
+    bias: Optional[torch.Tensor] = None,
+    alpha: float = 1.0,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """C = epilogue(alpha * a @ op(b)).  b_layout "nn": b is [K,N]; "nt": b is [N,K].
+
+    For epilogue "silu_mul", b holds packed gate/up columns (see pack_gate_up)
+    and the result has N/2 columns.
+    """
+    _require_gpu(a, b, bias, out)
+    if a.dtype not in (torch.float16, torch.bfloat16) or b.dtype != a.dtype:
+        raise HxmiError(f"gemm takes fp16 or bf16 operands of one dtype, got {a.dtype} and {b.dtype}")
+    if b_layout not in ("nn", "nt"):
+        raise HxmiError(f"b_layout must be 'nn' or 'nt', got {b_layout!r}")
+    if epilogue not in EPILOGUES:
+        raise HxmiError(f"unknown epilogue {epilogue!r}")
+    lda, ldb = _rowmajor(a, "a"), _rowmajor(b, "b")
+    M, K = a.shape
+    nt = b_layout == "nt"
+    N = b.shape[0] if nt else b.shape[1]
+    if (b.shape[1] if nt else b.shape[0]) != K:
+        raise HxmiError(f"inner dimensions differ: a {tuple(a.shape)}, b {tuple(b.shape)} ({b_layout})")
+    nout = N // 2 if epilogue == "silu_mul" else N
+    if epilogue in ("bias", "bias_gelu_tanh"):
+        bias = _vec(bias, N, a.dtype, "bias")
+        if bias is None:
+            raise HxmiError(f"epilogue {epilogue} needs a bias")
+    else:
+        bias = None
+    if out is None:
+        out = torch.empty((M, nout), dtype=a.dtype, device=a.device)
+    elif out.shape != (M, nout) or out.dtype != a.dtype:
+        raise HxmiError(f"out must be {a.dtype} {(M, nout)}")
+    ldc = _rowmajor(out, "out")
+    fn = load_library().hxmi_gemm_f16 if a.dtype == torch.float16 else load_library().hxmi_gemm_bf16
+    _check(fn(a.data_ptr(), b.data_ptr(), out.data_ptr(), _ptr(bias), M, N, K, lda, ldb, ldc, int(nt),
+              EPILOGUES[epilogue], float(alpha), _stream(a)))
+    return out
+
+
+def _batched(t: torch.Tensor, name: str) -> tuple[int, int]:
+    if t.dim() != 3:
+        raise HxmiError(f"{name} must be 3-D, got shape {tuple(t.shape)}")
+    if t.stride(2) != 1 and t.size(2) > 1:
+        raise HxmiError(f"{name} must have unit stride in its last dimension")
+    return max(t.stride(1), t.size(2), 1), t.stride(0)
+
+
+def bgemm(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    *,
+    b_layout: str = "nn",
+    epilogue: Optional[str] = None,
+    bias: Optional[torch.Tensor] = None,
+    alpha: float = 1.0,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Batched C[i] = epilogue(alpha * a[i] @ op(b[i])) over 3-D strided tensors."""
+    _require_gpu(a, b, bias, out)
+    if a.dtype not in (torch.float16, torch.bfloat16) or b.dtype != a.dtype:
+        raise HxmiError("bgemm takes fp16 or bf16 operands of one dtype")
+    if epilogue not in EPILOGUES:
+        raise HxmiError(f"unknown epilogue {epilogue!r}")
+    lda, sa = _batched(a, "a")
+    ldb, sb = _batched(b, "b")
+    batch, M, K = a.shape
+    nt = b_layout == "nt"
+    N = b.shape[1] if nt else b.shape[2]
+    if b.shape[0] != batch or (b.shape[2] if nt else b.shape[1]) != K:
+        raise HxmiError(f"shapes do not match: a {tuple(a.shape)}, b {tuple(b.shape)} ({b_layout})")
+    nout = N // 2 if epilogue == "silu_mul" else N
+    if epilogue in ("bias", "bias_gelu_tanh"):
+        bias = _vec(bias, N, a.dtype, "bias")
+        if bias is None:
+            raise HxmiError(f"epilogue {epilogue} needs a bias")
+    else:
+        bias = None
+    if out is None:
+        out = torch.empty((batch, M, nout), dtype=a.dtype, device=a.device)
+    ldc, sc = _batched(out, "out")
+    fn = load_library().hxmi_bgemm_f16 if a.dtype == torch.float16 else load_library().hxmi_bgemm_bf16
+    _check(fn(a.data_ptr(), b.data_ptr(), out.data_ptr(), _ptr(bias), batch, M, N, K, lda, ldb, ldc, sa, sb, sc,
+              int(nt), EPILOGUES[epilogue], float(alpha), _stream(a)))
+    return out
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           epilogue: Optional[str] = None) -> torch.Tensor:
+    """nn.Linear forward, y = x @ w.T (+ bias), with an optional fused activation.
+
+    epilogue: None, "gelu_tanh" or "silu_mul" (w then packed by pack_gate_up).
+    """
+    if epilogue is None:
+        epi = "bias" if bias is not None else None
+    elif epilogue == "gelu_tanh":
+        epi = "bias_gelu_tanh" if bias is not None else "gelu_tanh"
+    elif epilogue == "silu_mul":
+        if bias is not None:
+            raise HxmiError("silu_mul epilogue takes no bias")
+        epi = "silu_mul"
+    else:
+        raise HxmiError(f"unknown activation {epilogue!r}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    y = gemm(x2, w, b_layout="nt", epilogue=epi, bias=bias)
+    return y.reshape(*lead, y.shape[-1])
+
+
+def gemv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode linear y[M,N] = x[M,K] @ w[N,K].T (+ bias); HBM-streaming for M <= 16."""
+    _require_gpu(x, w, bias, out)
+    if x.dtype != torch.float16 or w.dtype != torch.float16:
+        raise HxmiError("gemv takes fp16 x and w")
+    ldx, ldw = _rowmajor(x, "x"), _rowmajor(w, "w")
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise HxmiError(f"x {tuple(x.shape)} and w {tuple(w.shape)} disagree on K")
+    bias = _vec(bias, N, torch.float16, "bias")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    ldy = _rowmajor(out, "out")
+    _check(load_library().hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, ldx, ldw,
+                                        ldy, _stream(x)))
+    return out
+
+
+def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Weight-only int8 linear: y = (x @ wq.T) * scale (+ bias); wq int8 [N,K], scale fp16 [N]."""
+    _require_gpu(x, wq, scale, bias, out)
+    if x.dtype != torch.float16 or wq.dtype != torch.int8:
+        raise HxmiError("w8a16_linear takes fp16 x and int8 wq")
+    ldx, ldw = _rowmajor(x, "x"), _rowmajor(wq, "wq")
+    M, K = x.shape
+    N = wq.shape[0]
+    if wq.shape[1] != K:
+        raise HxmiError(f"x {tuple(x.shape)} and wq {tuple(wq.shape)} disagree on K")
+    scale = _vec(scale, N, torch.float16, "scale")
+    bias = _vec(bias, N, torch.float16, "bias")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    ldy = _rowmajor(out, "out")
+    _check(load_library().hxmi_gemv_w8a16(x.data_ptr(), wq.data_ptr(), scale.data_ptr(), _ptr(bias), out.data_ptr(),
+                                          M, N, K, ldx, ldw, ldy, _stream(x)))
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RMSNorm over the last dim: weight * T(x * rsqrt(mean(x^2) + eps))."""
+    _require_gpu(x, weight, out)
+    if x.dtype not in (torch.float16, torch.bfloat16) or weight.dtype != x.dtype:
+        raise HxmiError("rms_norm takes fp16 or bf16 x and weight of the same dtype")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    ldx = _rowmajor(x2, "x")
+    rows, cols = x2.shape
+    weight = _vec(weight, cols, x.dtype, "weight")
+    if out is None:
+        out = torch.empty_like(x2)
+    out2 = out.reshape(rows, cols)
+    ldy = _rowmajor(out2, "out")
+    fn = load_library().hxmi_rmsnorm_f16 if x.dtype == torch.float16 else load_library().hxmi_rmsnorm_bf16
+    _check(fn(x2.data_ptr(), weight.data_ptr(), out2.data_ptr(), rows, cols, ldx, ldy, float(eps), _stream(x)))
+    return out2.reshape(*lead, cols)
+
+
+def softmax(x: torch.Tensor, scale: float = 1.0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(scale * x) over the last dim, fp32 math."""
+    _require_gpu(x, out)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise HxmiError("softmax takes fp16 or bf16 input")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    ldx = _rowmajor(x2, "x")
+    rows, cols = x2.shape
+    if out is None:
+        out = torch.empty_like(x2)
+    out2 = out.reshape(rows, cols)
+    ldy = _rowmajor(out2, "out")
+    fn = load_library().hxmi_softmax_f16 if x.dtype == torch.float16 else load_library().hxmi_softmax_bf16
+    _check(fn(x2.data_ptr(), out2.data_ptr(), rows, cols, ldx, ldy, float(scale), _stream(x)))
+    return out2.reshape(*lead, cols)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+    """SDPA as the reference lowers it (LowerTmTensor.cpp:91-250):
+    bmm(Q, K^T) * scale -> row softmax -> bmm(P, V); q, k, v are [..., S, D]."""
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    lead = q.shape[:-2]
+    S, D = q.shape[-2:]
+    q3 = q.reshape(-1, S, D)
+    k3 = k.reshape(-1, k.shape[-2], D)
+    v3 = v.reshape(-1, v.shape[-2], v.shape[-1])
+    s = bgemm(q3, k3, b_layout="nt", alpha=scale)
+    p = softmax(s)
+    o = bgemm(p, v3, b_layout="nn")
+    return o.reshape(*lead, S, v.shape[-1])
+
+
+def hexkl_matmul(act: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """hexkl_matmul_f16f16_f32 contract: fp32 out[n_row, n_col] = act[n_row, n_inner] @ w[n_inner, n_col]."""
+    _require_gpu(act, w)
+    if act.dtype != torch.float16 or w.dtype != torch.float16:
+        raise HxmiError("hexkl_matmul takes fp16 operands")
+    act = act.contiguous()
+    w = w.contiguous()
+    n_row, n_inner = act.shape
+    n_col = w.shape[1]
+    if w.shape[0] != n_inner:
+        raise HxmiError("inner dimensions differ")
+    out = torch.empty((n_row, n_col), dtype=torch.float32, device=act.device)
+    torch.cuda.current_stream(act.device).synchronize()
+    _check(load_library().hexkl_matmul_f16f16_f32(n_row, n_col, n_inner, out.data_ptr(), act.data_ptr(),
+                                                  w.data_ptr()))
+    return out
+
+
+def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """Interleave gate and up projections [I,K] into the packed [2I,K] layout the
+    SiLU-mul epilogue reads: rows [32q, 32q+16) = gate[16q:16q+16],
+    rows [32q+16, 32q+32) = up[16q:16q+16].  I must be a multiple of 16."""
+    if w_gate.shape != w_up.shape or w_gate.dim() != 2 or w_gate.shape[0] % 16:
+        raise HxmiError("gate and up must be [I, K] with I % 16 == 0")
+    inter, k = w_gate.shape
+    packed = torch.stack((w_gate.reshape(inter // 16, 16, k), w_up.reshape(inter // 16, 16, k)), dim=1)
+    return packed.reshape(2 * inter, k).contiguous()

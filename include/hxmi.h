@@ -1,0 +1,149 @@
+/*
+ * hxmi — C ABI of the MI355X (gfx950) hot-path kernels.
+ *
+ * Replaces, for one GPU, what Hexagon-MLIR's qcom_hexagon_backend generates
+ * and links for the matmul / GEMV / RMSNorm / softmax path: the compiled
+ * kernel entry `_mlir_ciface_<func>` that the Python launcher builds and runs
+ * (qcom_hexagon_backend/lib/Conversion/LinalgToLLVM/LinalgToLLVMPass.cpp:156-189,
+ * qcom_hexagon_backend/backend/torch_mlir_hexagon_launcher.py:258-306) and the
+ * runtime it calls (qcom_hexagon_backend/bin/runtime/include/HexagonCAPI.h:19-25,
+ * bin/runtime/UserDMA/RuntimeDMA.cc:48-96, bin/runtime/include/HexKLAPI.h:17-20).
+ *
+ * Conventions for every entry point:
+ *   - all tensor pointers are device pointers owned by the caller; nothing is
+ *     allocated or freed on these calls;
+ *   - matrices are row-major with explicit leading dimensions in elements;
+ *   - `stream` is a hipStream_t (NULL = the default stream); work is
+ *     stream-ordered and the call returns after the launch;
+ *   - return value: HXMI_OK, or an error code with a message available from
+ *     hxmi_last_error() (thread-local); invalid arguments are rejected before
+ *     anything is launched;
+ *   - a size of 0 in any output dimension is a no-op that returns HXMI_OK.
+ */
+#ifndef HXMI_H
+#define HXMI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp16 element type for the HexKL-compatible entry (ABI: a 2-byte value). */
+#if defined(__clang__) || (defined(__GNUC__) && __GNUC__ >= 12)
+typedef _Float16 hxmi_f16_t;
+#else
+typedef uint16_t hxmi_f16_t;
+#endif
+
+#define HXMI_OK 0
+#define HXMI_ERR_INVALID_ARGUMENT 1
+#define HXMI_ERR_UNSUPPORTED 2
+#define HXMI_ERR_HIP 3
+
+/* GEMM epilogues, applied to alpha * (A . op(B)) in fp32 before the store. */
+#define HXMI_EPI_NONE 0
+#define HXMI_EPI_BIAS 1           /* + bias[n]                                  */
+#define HXMI_EPI_SILU_MUL 2       /* silu(gate) * up over packed gate/up columns */
+#define HXMI_EPI_GELU_TANH 3      /* tanh-approximate GELU                       */
+#define HXMI_EPI_BIAS_GELU_TANH 4 /* GELU(x + bias[n])                           */
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* hxmi_last_error(void);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+int hxmi_version(void);
+
+/*
+ * C[M,N] = epilogue(alpha * A[M,K] . op(B)), fp32 accumulation, fp16 output.
+ *   b_is_nt = 0: B is [K,N] (linalg.matmul; reference config "C = A . B")
+ *   b_is_nt = 1: B is [N,K] (linalg.matmul_transpose_b; every nn.Linear)
+ * For HXMI_EPI_SILU_MUL, B holds N packed columns (N % 32 == 0): packed
+ * columns [32q, 32q+16) are gate rows 16q..16q+15 and [32q+16, 32q+32) the
+ * matching up rows; C receives N/2 columns, C[:, 16q+i] = silu(g_i) * u_i.
+ * bias (fp16, N entries) is required for the BIAS epilogues, else ignored.
+ * Replaces: the linalg.matmul / matmul_transpose_b lowering scheduled by
+ * ScheduleMatmulForHVXPass.cpp:69-195 and tiled by VTCMTiling.cpp:231-266
+ * (with HexmemCpyToDMA.cpp:120-271 DMA staging), plus the elementwise
+ * generics HexagonFusionPass leaves after it (FusionPass.cpp:161-179).
+ */
+int hxmi_gemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                  int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream);
+
+/* Same contract as hxmi_gemm_f16 with bf16 operands, bias and output. */
+int hxmi_gemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream);
+
+/*
+ * Strided batched GEMM: for b in [0,batch): C + b*strideC = epilogue(alpha *
+ * (A + b*strideA) . op(B + b*strideB)).  Strides in elements.
+ * Replaces: linalg.batch_matmul(_transpose_b) scheduling
+ * (ScheduleMatmulForHVXPass.cpp:105-167), used by the attention lowering
+ * LowerTmTensor.cpp:91-250 (Q.K^T scaled, then P.V).
+ */
+int hxmi_bgemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M, int64_t N,
+                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
+                   int64_t strideC, int b_is_nt, int epilogue, float alpha, void* stream);
+int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M, int64_t N,
+                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
+                    int64_t strideC, int b_is_nt, int epilogue, float alpha, void* stream);
+
+/*
+ * Decode GEMV/skinny GEMM: y[M,N] = x[M,K] . W[N,K]^T (+ bias[N]), fp16,
+ * fp32 accumulation, any M (M <= 16 streams W once through the GEMV kernel,
+ * larger M goes to the GEMM).  bias may be NULL.
+ * Replaces: the M = 1 matmul_transpose_b that the reference sends through
+ * the same generic HVX schedule (TilingPass.cpp:108-251); it has no GEMV.
+ */
+int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                  int64_t ldx, int64_t ldw, int64_t ldy, void* stream);
+
+/*
+ * Weight-only int8 linear: y[m,n] = scale[n] * sum_k x[m,k] * Wq[n,k] (+ bias[n]).
+ * x, scale, bias, y fp16; Wq int8 [N,K] (symmetric, per-output-channel
+ * scale).  Weights are converted to fp16 exactly in registers; the scale
+ * multiplies the fp32 sum.  Requires K % 16 == 0, ldw % 16 == 0, N % 4 == 0.
+ * Replaces: no reference kernel (only quant.qcast/dcast lowering to arith,
+ * LinalgToLLVMPass.cpp:203-209); defined by the weight-only int8 configs.
+ */
+int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const void* bias, void* y, int64_t M,
+                    int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* stream);
+
+/*
+ * RMSNorm per row: y = g * T(x * rsqrt(mean(x^2) + eps)), fp32 math, T = fp16
+ * (or bf16).  Replaces the HVX split-reduction lowering of the RMSNorm
+ * generic chain (SplitReductionUtils.cpp, TilingPass.cpp:261-289) whose
+ * semantics are test/python/triton/test_rms_norm.py:37-63 and HF LlamaRMSNorm.
+ */
+int hxmi_rmsnorm_f16(const void* x, const void* g, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy,
+                     float eps, void* stream);
+int hxmi_rmsnorm_bf16(const void* x, const void* g, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy,
+                      float eps, void* stream);
+
+/*
+ * Row softmax of scale * x: y = exp(s*x - max) / sum(exp(s*x - max)), fp32
+ * math.  Replaces the max/sub/exp/sum/div generic chain
+ * (qcom_hexagon_backend/test/Conversion/LinalgToLLVM/fusion_softmax_2D.mlir:8-57,
+ * LowerTmTensor.cpp:165-229) with its scale from the SDPA lowering.
+ */
+int hxmi_softmax_f16(const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float scale,
+                     void* stream);
+int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float scale,
+                      void* stream);
+
+/*
+ * HexKL-compatible matmul: outM[n_row, n_col] (fp32) = inAct[n_row, n_inner]
+ * . inW[n_inner, n_col] (both fp16, row-major, contiguous), device pointers,
+ * default stream, synchronous like the reference.  Returns 0 on success.
+ * Replaces: hexkl_matmul_f16f16_f32 (bin/runtime/include/HexKLAPI.h:17-20,
+ * bin/runtime/src/HexKLAPI.cpp:15-141), whose accumulator is read back as
+ * fp16; here it stays fp32.
+ */
+int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,
+                            const hxmi_f16_t* inW);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HXMI_H */

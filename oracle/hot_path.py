@@ -1,0 +1,299 @@
+"""Oracle: CPU restatement of the reference's hot-path op semantics.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU
+baseline, never as the product path (the product is libhxmi.so).
+
+Everything here is numpy, computed in float32 (float64 where an exact answer
+is wanted), following the reference files cited on each function.  The
+reference's own correctness oracle is PyTorch on x86
+(test/python/triton/test_matmul.py:90, test_rms_norm.py:85-87,
+test_softmax.py:91, test_silu.py:63, test_gelu.py:72,
+benchmark_models/micro_bench/test_matmul_benchmark.py:91-92); tests/ pin each
+function here against those torch CPU functions, against closed forms and
+against exact integer arithmetic.
+
+Parity status per function (how each is pinned, see tests/test_oracle.py):
+  matmul, linear, bmm         exact-integer known answers (golden fixtures
+                              from pure-Python integer loops), torch.matmul
+  gelu_tanh, silu, silu_mul   closed forms / special values, torch F.gelu
+                              (approximate="tanh") and F.silu
+  rms_norm, rms_norm_hf       closed forms (constant row, scale invariance),
+                              torch F.rms_norm
+  softmax                     row sums, shift invariance, uniform row,
+                              torch F.softmax
+  w8a16_linear, dequant_int8  exact integer one-hot known answers, scale
+                              linearity
+  sdpa                        composition of the above vs torch SDPA math
+  vtcm_tile_sizes             the reference's lit expectation
+                              (vtcm_tiling_static.mlir:80-88) and the
+                              footprint rule it encodes
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F32 = np.float32
+
+
+def _f32(x) -> np.ndarray:
+    return np.asarray(x).astype(F32)
+
+
+# ---- matmul family -----------------------------------------------------------
+
+
+def matmul(a, b, b_layout: str = "nn") -> np.ndarray:
+    """C = A . op(B) with fp16 inputs widened to fp32 and fp32 accumulation.
+
+    Follows the generic matmul body the reference tiles for HVX
+    (qcom_hexagon_backend/test/Conversion/LinalgToLLVM/vtcm_tiling_static.mlir
+    :62-68: extf f16->f32, mulf, addf) and the f32 CPU check of config 1
+    (benchmark_models/micro_bench/test_matmul_benchmark.py:22-31, 91-92).
+    b_layout "nt" is linalg.matmul_transpose_b
+    (lib/Transforms/ScheduleMatmulForHVXPass.cpp:78-139).
+    """
+    a32, b32 = _f32(a), _f32(b)
+    if b_layout == "nt":
+        b32 = b32.T
+    return a32 @ b32
+
+
+def linear(x, w, bias=None) -> np.ndarray:
+    """nn.Linear: x . w^T (+ bias), fp32."""
+    y = matmul(x, w, "nt")
+    if bias is not None:
+        y = y + _f32(bias)
+    return y
+
+
+def bmm(a, b, b_layout: str = "nn") -> np.ndarray:
+    """Batched matmul over the leading dim (linalg.batch_matmul[_transpose_b])."""
+    a32, b32 = _f32(a), _f32(b)
+    if b_layout == "nt":
+        b32 = np.swapaxes(b32, -1, -2)
+    return np.matmul(a32, b32)
+
+
+# ---- elementwise epilogues -----------------------------------------------------
+
+
+def silu(x) -> np.ndarray:
+    """x / (1 + exp(-x)) (test/python/triton/test_silu.py:35-45)."""
+    x = _f32(x)
+    return x / (F32(1) + np.exp(-x))
+
+
+def gelu_tanh(x) -> np.ndarray:
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))): the tanh form of
+    test/python/triton/test_gelu.py:25-53 and benchmark_models/run_vit.py:125
+    ("gelu_new"), checked against F.gelu(approximate="tanh") (test_gelu.py:72)."""
+    x = _f32(x)
+    k0 = F32(math.sqrt(2.0 / math.pi))
+    return F32(0.5) * x * (F32(1) + np.tanh(k0 * (x + F32(0.044715) * x * x * x)))
+
+
+def silu_mul_linear(x, w_gate, w_up) -> np.ndarray:
+    """HF LlamaMLP front half: silu(x . Wg^T) * (x . Wu^T)."""
+    return silu(linear(x, w_gate)) * linear(x, w_up)
+
+
+def gemm_epilogue(a, b, b_layout="nt", epilogue=None, bias=None, alpha=1.0) -> np.ndarray:
+    """alpha * A . op(B) followed by the fused epilogue, all fp32.
+
+    For "silu_mul", B holds packed gate/up columns (pack_gate_up)."""
+    y = matmul(a, b, b_layout) * F32(alpha)
+    if epilogue in (None, "none"):
+        return y
+    if epilogue == "bias":
+        return y + _f32(bias)
+    if epilogue == "gelu_tanh":
+        return gelu_tanh(y)
+    if epilogue == "bias_gelu_tanh":
+        return gelu_tanh(y + _f32(bias))
+    if epilogue == "silu_mul":
+        n = y.shape[-1]
+        g, u = unpack_gate_up_cols(y, n)
+        return silu(g) * u
+    raise ValueError(epilogue)
+
+
+def pack_gate_up(w_gate, w_up) -> np.ndarray:
+    """Packed [2I,K] layout: rows [32q,32q+16) = gate[16q:16q+16],
+    rows [32q+16,32q+32) = up[16q:16q+16]."""
+    wg, wu = np.asarray(w_gate), np.asarray(w_up)
+    i, k = wg.shape
+    return np.stack((wg.reshape(i // 16, 16, k), wu.reshape(i // 16, 16, k)), axis=1).reshape(2 * i, k)
+
+
+def unpack_gate_up_cols(y, n):
+    """Split packed output columns back into (gate, up), each n/2 wide."""
+    y = np.asarray(y)
+    lead = y.shape[:-1]
+    yy = y.reshape(*lead, n // 32, 2, 16)
+    return yy[..., 0, :].reshape(*lead, n // 2), yy[..., 1, :].reshape(*lead, n // 2)
+
+
+# ---- row reductions -----------------------------------------------------------------
+
+
+def rms_norm(x, g, eps: float = 1e-5) -> np.ndarray:
+    """fp32 reference RMSNorm, y = x / sqrt(mean(x^2) + eps) * g
+    (test/python/triton/test_rms_norm.py:52-60, checked there against
+    F.rms_norm at :85-87)."""
+    x32 = _f32(x)
+    ms = np.mean(x32 * x32, axis=-1, keepdims=True, dtype=np.float64).astype(F32)
+    return x32 / np.sqrt(ms + F32(eps)) * _f32(g)
+
+
+def rms_norm_hf(x, g, eps: float = 1e-5) -> np.ndarray:
+    """HF LlamaRMSNorm order (what benchmark_models/run_tinyllama.py runs):
+    normalise in fp32, round to fp16, multiply by the fp16 weight in fp16.
+    Returns the fp16 result."""
+    x32 = _f32(x)
+    ms = np.mean(x32 * x32, axis=-1, keepdims=True, dtype=np.float64).astype(F32)
+    n16 = (x32 / np.sqrt(ms + F32(eps))).astype(np.float16)
+    return (n16.astype(F32) * _f32(g)).astype(np.float16)
+
+
+def softmax(x, scale: float = 1.0) -> np.ndarray:
+    """Row softmax of scale*x with max subtraction: max, sub, exp, sum, div
+    (qcom_hexagon_backend/test/Conversion/LinalgToLLVM/fusion_softmax_2D.mlir
+    :8-57; test/python/triton/test_softmax.py:60-66)."""
+    z = _f32(x) * F32(scale)
+    z = z - np.max(z, axis=-1, keepdims=True)
+    e = np.exp(z)
+    return e / np.sum(e, axis=-1, keepdims=True)
+
+
+def sdpa(q, k, v, scale=None) -> np.ndarray:
+    """Attention as lib/Transforms/LowerTmTensor.cpp:91-250 lowers
+    tm_tensor.attention: bmm(Q, K^T) * scale -> softmax -> bmm(P, V)
+    (scale 1/sqrt(d), qcom_hexagon_backend/test/Conversion/TmTensorToLinalg/
+    SDPA.mlir:18-31)."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(np.asarray(q).shape[-1])
+    s = bmm(q, k, "nt")
+    p = softmax(s, scale)
+    return np.matmul(p, _f32(v))
+
+
+# ---- weight-only int8 ----------------------------------------------------------------
+
+
+def dequant_int8(q) -> np.ndarray:
+    """Integer weights as floats; exact for every int8 code."""
+    return np.asarray(q).astype(np.int32).astype(F32)
+
+
+def w8a16_linear(x, q, s, bias=None) -> np.ndarray:
+    """y = x . (q * s[:,None])^T (+ bias), fp32: the weight-only int8 config
+    (no reference kernel exists; only quant.qcast/dcast lowering,
+    lib/Conversion/LinalgToLLVM/LinalgToLLVMPass.cpp:203-209)."""
+    w = dequant_int8(q) * _f32(s)[:, None]
+    y = _f32(x) @ w.T
+    if bias is not None:
+        y = y + _f32(bias)
+    return y
+
+
+# ---- VTCM tile-size model ------------------------------------------------------------
+
+VTCM_BYTES = 2 * 1024 * 1024  # include/hexagon/Conversion/LinalgToLLVM/Common.h:26
+HVX_VECTOR_BYTES = 128  # lib/Conversion/LinalgToLLVM/Common.cpp:80-85 (native vector width)
+
+
+def _footprint(tile, operand_dims, elem_bytes) -> int:
+    # Sum over operands of (element size x product of the tile extents its
+    # indexing map reads); a constant-0 map result counts as extent 1
+    # (VTCMTilingOptions.cpp:98-117, 125-134).
+    return sum(eb * math.prod(tile[d] for d in od) for od, eb in zip(operand_dims, elem_bytes))
+
+
+def _reduction_factor(size: int, budget: int) -> int:
+    # Next power of two of size/budget, 1 when it already fits
+    # (VTCMTilingOptions.cpp:169-184).
+    if size < budget:
+        return 1
+    return 1 << math.ceil(math.log2(size / budget))
+
+
+def vtcm_tile_sizes(loop_ranges, operand_dims, elem_bytes, iterator_types, budget=VTCM_BYTES):
+    """Restatement of the reference's VTCM tile-size search, determineTileSizes
+    (lib/Conversion/LinalgToLLVM/VTCMTilingOptions.cpp:374-432).
+
+    loop_ranges:    static loop extents of the linalg op
+    operand_dims:   per operand (inputs then outputs), the loop indices its
+                    indexing map reads
+    elem_bytes:     per operand element size in bytes
+    iterator_types: per loop, "parallel" or "reduction"
+
+    Returns the tile sizes, or None when even unit tiles do not fit.
+    """
+    ranges = list(loop_ranges)
+    size = _footprint(ranges, operand_dims, elem_bytes)
+    if size <= budget:
+        return ranges
+    # priority: parallel dims, then reduction dims, each ordered by the
+    # footprint left after halving that dim alone (:190-243)
+    order = []
+    for kind in ("parallel", "reduction"):
+        cand = []
+        for d, it in enumerate(iterator_types):
+            if it != kind:
+                continue
+            t = list(ranges)
+            t[d] //= 2
+            cand.append((_footprint(t, operand_dims, elem_bytes), d))
+        order += [d for _, d in sorted(cand)]
+    # lower bounds: outermost dim >= 4 (parallelisation factor), innermost dim
+    # >= one HVX vector of the smallest operand type (:283-313)
+    lower = [1] * len(ranges)
+    if ranges[0] >= 4:
+        lower[0] = 4
+    vec = HVX_VECTOR_BYTES // min(elem_bytes)
+    if ranges[-1] >= vec:
+        lower[-1] = vec
+    tile = list(ranges)
+    rf = _reduction_factor(size, budget)
+    for first_pass in (True, False):
+        for d in order:
+            lb = lower[d] if first_pass else 1
+            tile[d] = max(tile[d] // rf, lb)
+            updated = _footprint(tile, operand_dims, elem_bytes)
+            if updated <= budget:
+                return tile
+            rf = _reduction_factor(updated, budget)
+    return None
+
+
+def matmul_tile_sizes(m: int, n: int, k: int, in_bytes: int = 2, out_bytes: int = 4):
+    """determineTileSizes for linalg.matmul after ScheduleMatmulForHVX's
+    interchange to loop order (m, k, n) (lib/Transforms/LinalgUtils.cpp:67-83):
+    A reads (m,k), B reads (k,n), C reads (m,n)."""
+    return vtcm_tile_sizes([m, k, n], [(0, 1), (1, 2), (0, 2)], [in_bytes, in_bytes, out_bytes],
+                           ["parallel", "reduction", "parallel"])
+
+
+# ---- tolerance metric --------------------------------------------------------------
+
+
+def max_rel_err(out, ref, floor_frac: float = 1e-3) -> float:
+    """max_i |out_i - ref_i| / max(|ref_i|, floor), floor = floor_frac * rms(ref).
+
+    The floor keeps entries whose exact value is (near) zero from dividing by
+    ~0; it is 1e-3 of the output's RMS, far below any fp16 rounding of a
+    typical entry."""
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    if o.shape != r.shape:
+        raise ValueError(f"shape mismatch {o.shape} vs {r.shape}")
+    if r.size == 0:
+        return 0.0
+    if not np.all(np.isfinite(o)):
+        return float("inf")
+    rms = float(np.sqrt(np.mean(r * r)))
+    floor = max(floor_frac * rms, 1e-30)
+    return float(np.max(np.abs(o - r) / np.maximum(np.abs(r), floor)))

@@ -1,0 +1,107 @@
+"""CPU checks of the C ABI boundary: the library loads, exports exactly what
+include/hxmi.h declares, and rejects invalid arguments before any launch."""
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "hxmi.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    for n in ["hxmi_gemm_f16", "hxmi_bgemm_f16", "hxmi_gemv_f16", "hxmi_gemv_w8a16", "hxmi_rmsnorm_f16",
+              "hxmi_softmax_f16", "hexkl_matmul_f16f16_f32", "hxmi_last_error"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.load_library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(declared_functions()) == set(pkg.hxmi.SIGNATURES)
+
+
+def test_version(pkg):
+    assert pkg.load_library().hxmi_version() >= 100
+
+
+def test_header_compiles_as_c(tmp_path):
+    import subprocess
+
+    src = tmp_path / "t.c"
+    src.write_text('#include "hxmi.h"\nint main(void){return hxmi_version() > 0 ? 0 : 1;}\n')
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-c", str(src), "-I", str(ROOT / "include"), "-o",
+                        str(tmp_path / "t.o")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+@pytest.mark.parametrize(
+    "args, msg",
+    [
+        ((None, None, None, None, -1, 8, 8, 8, 8, 8, 1, 0, 1.0, None), "negative size"),
+        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 2, 0, 1.0, None), "b_is_nt"),
+        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 9, 1.0, None), "unknown epilogue"),
+        ((1, 1, 1, None, 8, 48, 8, 8, 8, 48, 1, 2, 1.0, None), "SiLU-mul"),
+        ((None, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 0, 1.0, None), "null"),
+        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 1, 1.0, None), "bias"),
+        ((1, 1, 1, None, 8, 8, 16, 8, 16, 8, 1, 0, 1.0, None), "leading dimension"),
+    ],
+)
+def test_gemm_rejects_invalid_arguments(pkg, args, msg):
+    lib = pkg.load_library()
+    rc = lib.hxmi_gemm_f16(*args)
+    assert rc == 1
+    assert msg in lib.hxmi_last_error().decode()
+
+
+def test_empty_problems_are_noops(pkg):
+    lib = pkg.load_library()
+    assert lib.hxmi_gemm_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, 1, 0, 1.0, None) == 0
+    assert lib.hxmi_last_error() == b""
+    assert lib.hxmi_gemv_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, None) == 0
+    assert lib.hxmi_rmsnorm_f16(None, None, None, 0, 16, 16, 16, 1e-5, None) == 0
+    assert lib.hxmi_softmax_f16(None, None, 4, 0, 0, 0, 1.0, None) == 0
+
+
+def test_row_ops_reject_invalid(pkg):
+    lib = pkg.load_library()
+    assert lib.hxmi_rmsnorm_f16(1, None, 1, 4, 16, 16, 16, 1e-5, None) == 1  # no weight
+    assert lib.hxmi_softmax_f16(1, 1, 4, 16, 8, 16, 1.0, None) == 1  # ldx < cols
+    assert "leading dimension" in lib.hxmi_last_error().decode()
+
+
+def test_w8a16_rejects_unaligned_k(pkg):
+    lib = pkg.load_library()
+    assert lib.hxmi_gemv_w8a16(16, 16, 16, None, 16, 1, 8, 24, 24, 32, 8, None) == 1
+    assert "K % 16" in lib.hxmi_last_error().decode()
+
+
+def test_python_ops_refuse_cpu_tensors(pkg):
+    a = torch.zeros(8, 8, dtype=torch.float16)
+    with pytest.raises(pkg.HxmiError, match="GPU"):
+        pkg.gemm(a, a)
+    with pytest.raises(pkg.HxmiError, match="GPU"):
+        pkg.rms_norm(a, torch.ones(8, dtype=torch.float16))
+
+
+def test_error_is_thread_local(pkg):
+    import threading
+
+    lib = pkg.load_library()
+    lib.hxmi_gemm_f16(None, None, None, None, -1, 8, 8, 8, 8, 8, 1, 0, 1.0, None)
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(lib.hxmi_last_error()))
+    t.start()
+    t.join()
+    assert seen == [b""]
+    assert lib.hxmi_last_error() != b""

@@ -1,0 +1,173 @@
+"""GPU parity of the MFMA GEMM (through the C ABI) against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from gpu_util import TOL, f16_round, normal, np32, uniform
+from oracle import hot_path as ref
+
+pytestmark = pytest.mark.gpu
+
+TILES = list(range(7))  # TILE_256x256 .. TILE_64x64
+
+
+def run_gemm(pkg, dev, a, b, layout, **kw):
+    out = pkg.gemm(a.to(dev), b.to(dev), b_layout=layout, **kw)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("seed_a, seed_b", [(0, 1)])
+def test_config1_gemm_1024_nn(pkg, dev, seed_a, seed_b):
+    # single fp16 GEMM C = A.B, M=N=K=1024, U[-1,1], fp32 acc, fp16 out
+    a = uniform((1024, 1024), seed_a)
+    b = uniform((1024, 1024), seed_b)
+    c = run_gemm(pkg, dev, a, b, "nn")
+    assert ref.max_rel_err(np32(c), ref.matmul(a.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("tile", TILES)
+def test_gemm_exact_integer_every_tile(pkg, dev, force_tile, layout, tile):
+    d = np.load(GOLDEN / f"gemm_int_{layout}.npz")
+    force_tile(tile)
+    a = torch.from_numpy(d["a"]).half()
+    b = torch.from_numpy(d["b"]).half()
+    c = run_gemm(pkg, dev, a, b, layout)
+    assert np.array_equal(c.numpy(), f16_round(d["c"])), f"tile {tile}"
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_gemm_bias_exact_every_tile(pkg, dev, force_tile, tile):
+    d = np.load(GOLDEN / "gemm_int_epi.npz")
+    force_tile(tile)
+    a, b = torch.from_numpy(d["a"]).half(), torch.from_numpy(d["b"]).half()
+    bias = torch.from_numpy(d["bias"]).half()
+    c = run_gemm(pkg, dev, a, b, "nt", epilogue="bias", bias=bias.to(dev))
+    assert np.array_equal(c.numpy(), f16_round(d["c"]))
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (33, 72, 40), (130, 264, 200), (300, 136, 520), (197, 64, 64),
+                                   (64, 64, 0), (5, 24, 8)])
+@pytest.mark.parametrize("tile", [None, 0, 3, 6])
+def test_gemm_ragged_shapes(pkg, dev, force_tile, layout, M, N, K, tile):
+    force_tile(tile)
+    a = uniform((M, K), 2)
+    b = uniform((K, N) if layout == "nn" else (N, K), 3)
+    c = run_gemm(pkg, dev, a, b, layout)
+    assert ref.max_rel_err(np32(c), ref.matmul(a.numpy(), b.numpy(), layout)) <= TOL
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("M,N,K,lda", [(37, 45, 29, 29), (16, 16, 197, 197), (20, 33, 24, 31)])
+def test_gemm_unaligned_elementwise_path(pkg, dev, layout, M, N, K, lda):
+    a_full = uniform((M, lda), 4)
+    a = a_full[:, :K]
+    b = uniform((K, N) if layout == "nn" else (N, K), 5)
+    c = pkg.gemm(a_full.to(dev)[:, :K], b.to(dev), b_layout=layout)
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(c.cpu()), ref.matmul(a.numpy(), b.numpy(), layout)) <= TOL
+
+
+@pytest.mark.parametrize("epi", ["bias", "gelu_tanh", "bias_gelu_tanh"])
+@pytest.mark.parametrize("tile", [None, 0, 3, 6])
+def test_gemm_epilogues(pkg, dev, force_tile, epi, tile):
+    force_tile(tile)
+    M, N, K = 300, 264, 256
+    a = normal((M, K), 6)
+    w = normal((N, K), 7, 0.05)
+    bias = normal((N,), 8, 0.5)
+    c = run_gemm(pkg, dev, a, w, "nt", epilogue=epi, bias=bias.to(dev))
+    exp = ref.gemm_epilogue(a.numpy(), w.numpy(), "nt", epi, bias.numpy())
+    assert ref.max_rel_err(np32(c), exp) <= TOL
+
+
+@pytest.mark.parametrize("tile", [None, 0, 1, 2, 3, 4])
+def test_gemm_silu_mul(pkg, dev, force_tile, tile):
+    force_tile(tile)
+    M, I, K = 200, 320, 256
+    x = normal((M, K), 9)
+    wg = normal((I, K), 10, 0.05)
+    wu = normal((I, K), 11, 0.05)
+    packed = pkg.pack_gate_up(wg.to(dev), wu.to(dev))
+    h = pkg.linear(x.to(dev), packed, epilogue="silu_mul")
+    torch.cuda.synchronize()
+    exp = ref.silu_mul_linear(x.numpy(), wg.numpy(), wu.numpy())
+    assert ref.max_rel_err(np32(h.cpu()), exp) <= TOL
+
+
+def test_gemm_alpha(pkg, dev):
+    a, b = uniform((64, 128), 12), uniform((96, 128), 13)
+    c = run_gemm(pkg, dev, a, b, "nt", alpha=0.125)
+    assert ref.max_rel_err(np32(c), 0.125 * ref.matmul(a.numpy(), b.numpy(), "nt")) <= TOL
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_gemm_bf16(pkg, dev, layout):
+    a = uniform((256, 320), 14, dtype=torch.bfloat16)
+    b = uniform((320, 192) if layout == "nn" else (192, 320), 15, dtype=torch.bfloat16)
+    c = run_gemm(pkg, dev, a, b, layout)
+    # bf16 output rounding is 2^-9 relative
+    assert ref.max_rel_err(np32(c), ref.matmul(np32(a), np32(b), layout)) <= TOL
+
+
+def test_gemm_strided_views(pkg, dev):
+    base = uniform((128, 200), 16)
+    a = base[:, 8:136]  # lda = 200, 16-byte aligned rows
+    b = uniform((128, 96), 17)
+    c = pkg.gemm(base.to(dev)[:, 8:136], b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(c.cpu()), ref.matmul(a.numpy(), b.numpy())) <= TOL
+
+
+def test_gemm_output_view_untouched_outside(pkg, dev):
+    a, b = uniform((40, 64), 18), uniform((64, 48), 19)
+    out = torch.full((40, 64), 7.0, dtype=torch.float16, device=dev)
+    pkg.gemm(a.to(dev), b.to(dev), out=out[:, :48])
+    torch.cuda.synchronize()
+    o = out.cpu()
+    assert torch.all(o[:, 48:] == 7.0)
+    assert ref.max_rel_err(np32(o[:, :48]), ref.matmul(a.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_gemm_4096_cube(pkg, dev, layout):
+    a = uniform((4096, 4096), 20)
+    b = uniform((4096, 4096), 21)
+    c = run_gemm(pkg, dev, a, b, layout)
+    assert ref.max_rel_err(np32(c), ref.matmul(a.numpy(), b.numpy(), layout)) <= TOL
+
+
+@pytest.mark.parametrize("name,N,K", [("qkv", 2560, 2048), ("o", 2048, 2048), ("down", 2048, 5632)])
+def test_tinyllama_projections(pkg, dev, name, N, K):
+    x = normal((512, K), 22)
+    w = normal((N, K), 23, 0.02)
+    y = run_gemm(pkg, dev, x, w, "nt")
+    assert ref.max_rel_err(np32(y), ref.linear(x.numpy(), w.numpy())) <= TOL
+
+
+def test_bgemm_vit_attention_products(pkg, dev):
+    q = normal((96, 197, 64), 24)
+    k = normal((96, 197, 64), 25)
+    v = normal((96, 197, 64), 26)
+    s = pkg.bgemm(q.to(dev), k.to(dev), b_layout="nt", alpha=0.125)
+    p = pkg.softmax(s)
+    o = pkg.bgemm(p, v.to(dev), b_layout="nn")
+    torch.cuda.synchronize()
+    s_ref = 0.125 * ref.bmm(q.numpy(), k.numpy(), "nt")
+    assert ref.max_rel_err(np32(s.cpu()), s_ref) <= TOL
+    o_ref = ref.sdpa(q.numpy(), k.numpy(), v.numpy(), 0.125)
+    assert ref.max_rel_err(np32(o.cpu()), o_ref) <= TOL
+
+
+def test_hexkl_compat_matmul(pkg, dev):
+    # hexkl_linalg_matmul/wrapper.cpp:30-67: 1024x64 . 64x512, N(0,0.5)
+    # rounded to 4 decimals, |diff| <= 1e-2 against a CPU triple loop
+    act = torch.round(normal((1024, 64), 27, 0.5, torch.float32) * 1e4) / 1e4
+    w = torch.round(normal((64, 512), 28, 0.5, torch.float32) * 1e4) / 1e4
+    act, w = act.half(), w.half()
+    out = pkg.hexkl_matmul(act.to(dev), w.to(dev)).cpu()
+    assert out.dtype == torch.float32
+    assert np.max(np.abs(out.numpy() - ref.matmul(act.numpy(), w.numpy()))) <= 1e-2

@@ -1,0 +1,85 @@
+"""GPU parity of the RMSNorm and softmax row kernels."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, normal, np32, uniform
+from oracle import hot_path as ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,cols", [(512, 2048), (127, 513), (3, 8), (64, 4096), (5, 8200), (1, 520)])
+def test_rmsnorm(pkg, dev, rows, cols):
+    x = normal((rows, cols), 1)
+    g = (1 + normal((cols,), 2, 0.02, torch.float32)).half()
+    y = pkg.rms_norm(x.to(dev), g.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert ref.max_rel_err(y.astype(np.float32), ref.rms_norm(x.numpy(), g.numpy(), 1e-5)) <= TOL
+    # HF order (round the normalised value to fp16 before the weight): within
+    # one fp16 ulp of the oracle's HF-order result
+    hf = ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-5).astype(np.float32)
+    assert np.max(np.abs(y.astype(np.float32) - hf) / np.maximum(np.abs(hf), 1e-3)) <= 2 ** -9
+
+
+def test_rmsnorm_reference_test_shape_uniform(pkg, dev):
+    # test_rms_norm.py:19-20, 65-67: 127 x 513, rand inputs and weights
+    x = uniform((127, 513), 3, 0, 1)
+    g = uniform((513,), 4, 0, 1)
+    y = pkg.rms_norm(x.to(dev), g.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(np32(y.cpu()) - ref.rms_norm(x.numpy(), g.numpy(), 1e-5))) <= 1e-2
+
+
+def test_rmsnorm_constant_and_zero_rows(pkg, dev):
+    x = torch.zeros((4, 256), dtype=torch.float16)
+    x[1] = 3.0
+    g = torch.ones(256, dtype=torch.float16)
+    y = pkg.rms_norm(x.to(dev), g.to(dev), 1e-5).cpu().numpy().astype(np.float32)
+    assert not np.any(y[0]) and not np.any(y[2:])
+    assert np.allclose(y[1], 3.0 / np.sqrt(9.0 + 1e-5), rtol=2 ** -10)
+
+
+def test_rmsnorm_bf16(pkg, dev):
+    x = normal((64, 2048), 5, dtype=torch.bfloat16)
+    g = (1 + normal((2048,), 6, 0.02, torch.float32)).to(torch.bfloat16)
+    y = pkg.rms_norm(x.to(dev), g.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.rms_norm(np32(x), np32(g), 1e-6)) <= TOL
+
+
+@pytest.mark.parametrize("rows,cols,scale", [(96 * 197, 197, 0.125), (128, 128, 1.0), (7, 3000, 0.5), (33, 1, 1.0),
+                                             (5, 64, 2.0), (9, 1024, 1.0)])
+def test_softmax(pkg, dev, rows, cols, scale):
+    x = normal((rows, cols), 7)
+    y = pkg.softmax(x.to(dev), scale)
+    torch.cuda.synchronize()
+    y = np32(y.cpu())
+    assert ref.max_rel_err(y, ref.softmax(x.numpy(), scale)) <= TOL
+    assert np.allclose(y.sum(-1), 1.0, atol=2e-3)
+
+
+def test_softmax_reference_test_tolerance(pkg, dev):
+    # test_softmax.py:19-21, 91-94: 128 x 128 rand, atol 1e-3 for fp16
+    x = uniform((128, 128), 8, 0, 1)
+    y = pkg.softmax(x.to(dev))
+    torch.cuda.synchronize()
+    assert np.max(np.abs(np32(y.cpu()) - ref.softmax(x.numpy()))) <= 1e-3
+
+
+def test_softmax_shift_invariance_and_uniform(pkg, dev):
+    x = normal((16, 197), 9)
+    y1 = pkg.softmax(x.to(dev))
+    y2 = pkg.softmax((x.float() + 3.0).half().to(dev))
+    u = pkg.softmax(torch.zeros((4, 197), dtype=torch.float16, device=dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y2.cpu()), np32(y1.cpu())) <= TOL
+    assert np.allclose(np32(u.cpu()), 1 / 197, rtol=2 ** -10)
+
+
+def test_softmax_bf16(pkg, dev):
+    x = normal((64, 197), 10, dtype=torch.bfloat16)
+    y = pkg.softmax(x.to(dev), 0.125)
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.softmax(np32(x), 0.125)) <= TOL
