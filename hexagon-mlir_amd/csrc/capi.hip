@@ -47,7 +47,7 @@ int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bi
   if (batch == 0 || M == 0 || nout == 0) return ok();
   REQUIRE(epilogue != HXMI_EPI_SILU_MUL || N % 32 == 0, "%s: SiLU-mul needs N %% 32 == 0 (packed gate/up), got %lld",
           name, (long long)N);
-  REQUIRE(A && B && C, "%s: null operand pointer", name);
+  REQUIRE(C && ((A && B) || K == 0), "%s: null operand pointer", name);
   REQUIRE(bias || (epilogue != HXMI_EPI_BIAS && epilogue != HXMI_EPI_BIAS_GELU_TANH),
           "%s: epilogue %d needs a bias pointer", name, epilogue);
   REQUIRE(lda >= K && ldb >= (b_is_nt ? K : N) && ldc >= nout, "%s: leading dimension too small (lda=%lld ldb=%lld ldc=%lld)",

@@ -11,11 +11,14 @@
 //   * out-of-range rows / k-chunks use an offset past the buffer resource's
 //     range, so the hardware returns zeros and no tail branches are needed;
 //   * LDS rows are XOR-swizzled in 16-byte chunks so MFMA fragment reads are
-//     bank-conflict free; a [K,N] (NN) operand is read with ds_read_b64_tr_b16;
+//     free of conflicts on gfx950's 64 LDS banks; a [K,N] (NN) operand is read
+//     with ds_read_b64_tr_b16;
 //   * the MFMA is issued as D[n][m] = B^T . A^T so every lane owns four
 //     consecutive output columns, which makes the fused epilogue (bias,
 //     SiLU-mul, tanh-GELU) and the LDS-staged 16-byte stores cheap.
 #pragma once
+
+#include <utility>
 
 #include "hxmi_common.h"
 #include "hxmi_internal.h"
@@ -79,13 +82,19 @@ __device__ __forceinline__ void map_tile(int bid, const KArgs& a, int& b, int& t
   tn = wi / gsz;
 }
 
-// Fragment of a k-contiguous tile stored as [rows][64] with 16-byte chunks
-// XOR-swizzled by (row & 7).  MFMA 32x32x16 operand layout: lane l holds row
-// (l % 32), k = 8*(l / 32) .. +7 of the 16-deep step s.
+// A k-contiguous tile is stored as [rows][64 elements]: 128-byte rows, two
+// rows per 256-byte line of the 64 4-byte LDS banks.  A ds_read_b128 phase
+// serves 16 lanes, which read the same 16-byte chunk of 16 consecutive rows;
+// XOR-ing the chunk index with (row >> 1) & 7 puts those 16 reads in 16
+// distinct bank groups.
+__device__ __forceinline__ int kc_swz(int r) { return (r >> 1) & 7; }
+
+// MFMA 32x32x16 operand layout: lane l holds row (l % 32), k = 8*(l / 32) .. +7
+// of the 16-deep step s.
 __device__ __forceinline__ short8v read_kc(const char* tile, int r_off, int s, int lane) {
   const int r = r_off + (lane & 31);
   const int c = (s << 1) + (lane >> 5);
-  return *(const short8v*)(tile + r * 128 + ((c ^ (r & 7)) << 4));
+  return *(const short8v*)(tile + r * 128 + ((c ^ kc_swz(r)) << 4));
 }
 
 template <int BN>
@@ -146,6 +155,39 @@ __device__ __forceinline__ short8v dequant8(int2v raw) {
   return out;
 }
 
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Instruction order inside one substep region (the compiler's scheduler
+// otherwise bunches the LDS reads right before the MFMAs that consume them):
+// the substep's NMF MFMAs with the NDS fragment reads of the next substep
+// and NVM global->LDS loads slotted between them.
+template <int NMF, int NDS, int NVM>
+__device__ __forceinline__ void schedule_substep() {
+  static_assert(NMF > 0, "substep without MFMAs");
+  constexpr int kMFMA = 0x008, kVMEMR = 0x020, kDSR = 0x100;
+  // reads go one per MFMA from the start of the region (they feed the next
+  // region); global loads are spread over the slots after them
+  constexpr int FREE = NMF > NDS ? NMF - NDS : 1;
+  static_for<NMF>([&](auto M) {
+    constexpr int m = decltype(M)::value;
+    __builtin_amdgcn_sched_group_barrier(kMFMA, 1, 0);
+    constexpr int nds = m < NDS ? ((m + 1 == NMF) ? NDS - m : 1) : 0;
+    if constexpr (nds > 0) __builtin_amdgcn_sched_group_barrier(kDSR, nds, 0);
+    constexpr int mv = m - (NMF - FREE);
+    constexpr int nv = mv >= 0 ? (mv + 1) * NVM / FREE - mv * NVM / FREE : 0;
+    if constexpr (nv > 0) __builtin_amdgcn_sched_group_barrier(kVMEMR, nv, 0);
+  });
+}
+
 template <int BM, int BN, int WM, int WN, bool NN, typename T, int EPI, bool OUTF32, bool BI8 = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
@@ -176,111 +218,108 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
                    : BI8 ? a.B + (b * a.sB + (int64_t)n0 * a.ldb)
                          : a.B + (b * a.sB + (int64_t)n0 * a.ldb) * 2;
 
-  // ---- per-lane load plan -------------------------------------------------
+  // ---- load plan --------------------------------------------------------------
+  // Each wave instruction moves 1 KB (8 rows of a k-contiguous tile, or
+  // 1024/(2*BN) rows of an NN tile).  One buffer resource per operand and
+  // K-step starts at the step's first column and ends (num_records) at the
+  // last valid row, so rows past M / N / K read as zero.  The only per-lane
+  // state is one byte offset per operand; a chunk past K swaps it for kOOB.
   constexpr int IA = BM / 8 / NW;
-  uint32_t offA[IA];
-  bool okA[IA];
-  const int cA = (lane & 7) ^ (lane >> 3);
-#pragma unroll
-  for (int i = 0; i < IA; ++i) {
-    const int row = (i * NW + w) * 8 + (lane >> 3);
-    okA[i] = (m0 + row) < a.M;
-    offA[i] = (uint32_t)(row * a.lda * 2 + cA * 16);
-  }
+  // lane l of an instruction fills slot (row (l >> 3), position l & 7) of its
+  // 8-row block, so it loads logical chunk position ^ kc_swz(row); with an even
+  // wave count that only depends on the wave's parity and l >> 4
+  static_assert(NW % 2 == 0, "even wave count");
+  const int cA = (lane & 7) ^ (((w & 1) << 2) | (lane >> 4));
+  const uint32_t voffA = (uint32_t)((w * 8 + (lane >> 3)) * a.lda * 2 + cA * 16);
+  const uint32_t stepA = (uint32_t)(NW * 8 * a.lda * 2);  // bytes between a wave's A instructions
+  const uint32_t bytesA = (uint32_t)(min(BM, a.M - m0) * a.lda * 2);
 
-  constexpr int CPR = BN / 8;                              // NN: 16-byte chunks per k-row
-  constexpr int RPI = NN ? (1024 / (BN * 2)) : 8;          // rows per wave instruction
-  constexpr int IB = NN ? (BK / RPI / NW) : (BN / 8 / NW);
+  constexpr int CPR = BN / 8;                          // NN: 16-byte chunks per k-row
+  constexpr int RPI = NN ? (1024 / (BN * 2)) : 8;      // rows per wave instruction
+  constexpr int IB = BI8 ? 1 : (NN ? (BK / RPI / NW) : (BN / 8 / NW));
   static_assert(IB >= 1, "B load plan");
-  uint32_t offB[IB];
-  bool okB[IB];
-  int rowB[IB];
-  int cB = 0;
-#pragma unroll
-  for (int i = 0; i < IB; ++i) {
-    if constexpr (NN) {
-      const int row = (i * NW + w) * RPI + lane / CPR;
-      const int c = (lane % CPR) ^ nn_swz<BN>(row);
-      rowB[i] = row;
-      okB[i] = (n0 + c * 8) < a.N;
-      offB[i] = (uint32_t)(row * a.ldb * 2 + c * 16);
-    } else {
-      const int row = (i * NW + w) * 8 + (lane >> 3);
-      cB = cA;
-      rowB[i] = row;
-      okB[i] = (n0 + row) < a.N;
-      offB[i] = (uint32_t)(row * a.ldb * 2 + cA * 16);
-    }
+  uint32_t voffB, stepB, bytesB;
+  if constexpr (NN) {
+    const int rowl = w * RPI + lane / CPR;  // (row & 3) is the same for every instruction
+    const int c = (lane % CPR) ^ nn_swz<BN>(rowl);
+    voffB = (n0 + c * 8) < a.N ? (uint32_t)(rowl * a.ldb * 2 + c * 16) : kOOB;
+    stepB = (uint32_t)(NW * RPI * a.ldb * 2);
+    bytesB = (uint32_t)(a.ldb * 2);  // per valid k-row
+  } else {
+    voffB = (uint32_t)((w * 8 + (lane >> 3)) * a.ldb * (BI8 ? 1 : 2) + cA * 16);
+    stepB = (uint32_t)(NW * 8 * a.ldb * 2);
+    bytesB = (uint32_t)(min(BN, a.N - n0) * a.ldb * (BI8 ? 1 : 2));
   }
+  const int nk = (K + BK - 1) / BK;
 
   // int8 B: register-staged, 16 weights (one row, 16 k) per 16-byte load,
   // dequantised to fp16 on the way into the same swizzled LDS layout.
   constexpr int I8L = BI8 ? (BN * 4 + NT - 1) / NT : 1;
-  uint32_t offQ[I8L];
-  int rowQ[I8L], qQ[I8L];
-  bool okQ[I8L];
   int4v regQ[I8L];
-  if constexpr (BI8) {
+  auto load_q = [&](int kt) {
+    const int k0 = kt * BK;
+    const uint32_t nr = kt < nk ? bytesB - (uint32_t)k0 : 0u;
+    const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Bb + k0, nr);
 #pragma unroll
     for (int i = 0; i < I8L; ++i) {
       const int idx = i * NT + threadIdx.x;
-      rowQ[i] = idx >> 2;
-      qQ[i] = idx & 3;
-      okQ[i] = idx < BN * 4 && (n0 + rowQ[i]) < a.N;
-      offQ[i] = (uint32_t)(rowQ[i] * a.ldb + qQ[i] * 16);
-    }
-  }
-  auto load_q = [&](int kt) {
-    const int k0 = kt * BK;
-    const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Bb + k0, 0x7fffffff);
-#pragma unroll
-    for (int i = 0; i < I8L; ++i) {
-      const bool ok = okQ[i] && (k0 + qQ[i] * 16) < K;
-      regQ[i] = load16(rQ, ok ? offQ[i] : kOOB);
+      const int r = idx >> 2, q = idx & 3;
+      const bool ok = idx < BN * 4 && (k0 + q * 16) < K;
+      regQ[i] = load16(rQ, ok ? (uint32_t)(r * a.ldb + q * 16) : kOOB);
     }
   };
   auto store_q = [&](int stage) {
     char* sB_ = smem + stage * STAGE + A_BYTES;
 #pragma unroll
     for (int i = 0; i < I8L; ++i) {
-      if (BN * 4 % NT == 0 || i * NT + (int)threadIdx.x < BN * 4) {
-        const int r = rowQ[i];
+      const int idx = i * NT + threadIdx.x;
+      if (BN * 4 % NT == 0 || idx < BN * 4) {
+        const int r = idx >> 2, q = idx & 3;
         const short8v lo = dequant8(int2v{regQ[i][0], regQ[i][1]});
         const short8v hi = dequant8(int2v{regQ[i][2], regQ[i][3]});
-        *(short8v*)(sB_ + r * 128 + (((2 * qQ[i]) ^ (r & 7)) << 4)) = lo;
-        *(short8v*)(sB_ + r * 128 + (((2 * qQ[i] + 1) ^ (r & 7)) << 4)) = hi;
+        *(short8v*)(sB_ + r * 128 + (((2 * q) ^ kc_swz(r)) << 4)) = lo;
+        *(short8v*)(sB_ + r * 128 + (((2 * q + 1) ^ kc_swz(r)) << 4)) = hi;
       }
     }
   };
 
+  // Loads of K-step kt into LDS stage `stage`; a step past the end issues
+  // loads against an empty buffer (all zeros, nothing touched).
   auto issue = [&](int kt, int stage) {
     const int k0 = kt * BK;
+    const bool live = kt < nk;
     char* sA_ = smem + stage * STAGE;
     char* sB_ = sA_ + A_BYTES;
-    const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (int64_t)k0 * 2, 0x7fffffff);
-    const bool kokA = (k0 + cA * 8) < K;
+    const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (int64_t)k0 * 2, live ? bytesA - 2u * k0 : 0u);
+    const uint32_t vA = (k0 + cA * 8) < K ? voffA : kOOB;
 #pragma unroll
-    for (int i = 0; i < IA; ++i) {
-      const int rb = (i * NW + w) * 8;
-      load_lds16(rA, (HXMI_LDS void*)to_lds(sA_ + rb * 128), (okA[i] && kokA) ? offA[i] : kOOB);
-    }
+    for (int i = 0; i < IA; ++i)
+      load_lds16(rA, (HXMI_LDS void*)to_lds(sA_ + (i * NW + w) * 1024), vA + i * stepA);
     if constexpr (NN) {
-      const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + (int64_t)k0 * a.ldb * 2, 0x7fffffff);
+      const uint32_t rows = (uint32_t)min(BK, K - k0);
+      const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + (int64_t)k0 * a.ldb * 2, live ? rows * bytesB : 0u);
 #pragma unroll
-      for (int i = 0; i < IB; ++i) {
-        const int rb = (i * NW + w) * RPI;
-        const bool ok = okB[i] && (k0 + rowB[i]) < K;
-        load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + rb * (BN * 2)), ok ? offB[i] : kOOB);
-      }
+      for (int i = 0; i < IB; ++i)
+        load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + (i * NW + w) * 1024), voffB + i * stepB);
     } else if constexpr (!BI8) {
-      const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + (int64_t)k0 * 2, 0x7fffffff);
-      const bool kokB = (k0 + cB * 8) < K;
+      const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + (int64_t)k0 * 2, live ? bytesB - 2u * k0 : 0u);
+      const uint32_t vB = (k0 + cA * 8) < K ? voffB : kOOB;
 #pragma unroll
-      for (int i = 0; i < IB; ++i) {
-        const int rb = (i * NW + w) * 8;
-        load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + rb * 128), (okB[i] && kokB) ? offB[i] : kOOB);
-      }
+      for (int i = 0; i < IB; ++i)
+        load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + (i * NW + w) * 1024), vB + i * stepB);
     }
+  };
+
+  auto read_frags = [&](short8v (&fa)[TM], short8v (&fb)[TN], const char* sA_, const char* sB_, int s) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      if constexpr (NN)
+        fb[i] = read_nn<BN>(sB_, wn * WN + i * 32, s, lane);
+      else
+        fb[i] = read_kc(sB_, wn * WN + i * 32, s, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) fa[j] = read_kc(sA_, wm * WM + j * 32, s, lane);
   };
 
   float16v acc[TN][TM];
@@ -289,44 +328,54 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = float16v{};
 
-  const int nk = (K + BK - 1) / BK;
-  if (nk > 0) {
-    issue(0, 0);
-    if constexpr (BI8) {
-      load_q(0);
-      store_q(0);
-    }
+  // Software pipeline over K-steps (two LDS stages, fragments double
+  // buffered in registers).  Per K-step kt, in stage kt&1:
+  //   substeps 0..2: MFMAs of substep s, reads of substep s+1 in between;
+  //   then: wait for step kt+1's loads, barrier (step kt+1 visible; every
+  //   wave has read all of step kt), refill stage kt&1 with step kt+2;
+  //   substep 3: MFMAs, with step kt+1's first fragments and step kt+2's
+  //   global loads in between.
+  constexpr int SUBS = BK / 16;
+  constexpr int NDS = (NN ? 2 * TN : TN) + TM;  // LDS read instructions per substep
+  constexpr int NVM = BI8 ? IA : IA + IB;       // global->LDS loads per K-step
+  issue(0, 0);
+  issue(1, 1);
+  if constexpr (BI8) {
+    load_q(0);
+    store_q(0);
+    load_q(1);
   }
+  wait_vmcnt0();
+  __syncthreads();
+  short8v fa[2][TM], fb[2][TN];
+  read_frags(fa[0], fb[0], smem, smem + A_BYTES, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    wait_vmcnt0();
-    __syncthreads();
-    if (kt + 1 < nk) {
-      issue(kt + 1, (kt + 1) & 1);
-      if constexpr (BI8) load_q(kt + 1);
-    }
-    const char* sA_ = smem + (kt & 1) * STAGE;
+    const int cur = kt & 1;
+    const char* sA_ = smem + cur * STAGE;
     const char* sB_ = sA_ + A_BYTES;
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      short8v bf[TN], af[TM];
-#pragma unroll
-      for (int i = 0; i < TN; ++i) {
-        if constexpr (NN)
-          bf[i] = read_nn<BN>(sB_, wn * WN + i * 32, s, lane);
-        else
-          bf[i] = read_kc(sB_, wn * WN + i * 32, s, lane);
+    static_for<SUBS>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      constexpr int nxt = (s + 1) & 1;
+      if constexpr (s + 1 < SUBS) {
+        read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1);
+        if constexpr (BI8 && s == 1) store_q(cur ^ 1);
+      } else {
+        wait_vmcnt0();
+        __syncthreads();
+        issue(kt + 2, cur);
+        if constexpr (BI8) load_q(kt + 2);
+        read_frags(fa[nxt], fb[nxt], smem + (cur ^ 1) * STAGE, smem + (cur ^ 1) * STAGE + A_BYTES, 0);
       }
-#pragma unroll
-      for (int j = 0; j < TM; ++j) af[j] = read_kc(sA_, wm * WM + j * 32, s, lane);
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(bf[i], af[j], acc[i][j]);
-    }
-    if constexpr (BI8) {
-      if (kt + 1 < nk) store_q((kt + 1) & 1);
-    }
+        for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[s & 1][i], fa[s & 1][j], acc[i][j]);
+      schedule_substep<TN * TM, NDS, (s + 1 < SUBS) ? 0 : NVM>();
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
+  wait_vmcnt0();
+  __syncthreads();
 
   // ---- epilogue -------------------------------------------------------------
   const float alpha = a.alpha;

@@ -297,3 +297,20 @@ def max_rel_err(out, ref, floor_frac: float = 1e-3) -> float:
     rms = float(np.sqrt(np.mean(r * r)))
     floor = max(floor_frac * rms, 1e-30)
     return float(np.max(np.abs(o - r) / np.maximum(np.abs(r), floor)))
+
+
+def max_err_vs_scale(out, ref) -> float:
+    """max_i |out_i - ref_i| / max_i |ref_i|: the error relative to the
+    output's scale.  Used for multi-kernel pipelines whose fp16
+    intermediates (as the reference's own decomposed lowering materialises
+    them, e.g. S and P of attention) leave ~1e-4 absolute noise that an
+    elementwise ratio would magnify at outputs that cancel to ~0."""
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    if o.shape != r.shape:
+        raise ValueError(f"shape mismatch {o.shape} vs {r.shape}")
+    if r.size == 0:
+        return 0.0
+    if not np.all(np.isfinite(o)):
+        return float("inf")
+    return float(np.max(np.abs(o - r)) / max(float(np.max(np.abs(r))), 1e-30))
