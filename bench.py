@@ -58,6 +58,7 @@ class Timer:
         self.torch = torch
 
     def per_iter_ms(self, fn, iters: int, warmup: int = 3) -> float:
+        """Eager launches (host launch cost included when it dominates)."""
         torch = self.torch
         for _ in range(warmup):
             fn(0)
@@ -70,6 +71,39 @@ class Timer:
         e.record()
         torch.cuda.synchronize()
         return s.elapsed_time(e) / iters
+
+    def capture(self, fn, n: int):
+        """HIP graph of fn(0) .. fn(n-1), captured after eager warm-up."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(min(n, 3)):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        return g
+
+    def graph_ms(self, fn, n: int, replays: int = 3) -> float:
+        """Per-call time of fn from replays of a graph of n back-to-back calls
+        (launch cost reduced to the GPU's own dispatch), HIP events on the
+        stream the replays run on."""
+        torch = self.torch
+        g = self.capture(fn, n)
+        g.replay()
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(replays):
+            g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / (n * replays)
 
 
 def make_block(pkg, torch, dev):
@@ -111,7 +145,7 @@ def bench_gemm(pkg, torch, dev, timer, M, N, K, layout, iters):
     b = (torch.rand(K, N, generator=g) * 2 - 1).half().to(dev) if layout == "nn" else \
         (torch.rand(N, K, generator=g) * 2 - 1).half().to(dev)
     c = torch.empty(M, N, dtype=torch.float16, device=dev)
-    ms = timer.per_iter_ms(lambda i: pkg.gemm(a, b, b_layout=layout, out=c), iters)
+    ms = timer.graph_ms(lambda i: pkg.gemm(a, b, b_layout=layout, out=c), iters)
     tf = 2 * M * N * K / (ms * 1e-3) / 1e12
     return {"ms": round(ms, 5), "tflops": round(tf, 1), "frac_mfma_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
 
@@ -134,7 +168,7 @@ def bench_gemv(pkg, torch, dev, timer, M, K, N, int8, iters, min_bytes=768 << 20
         ws = [torch.empty(N, K, dtype=torch.float16, device=dev).normal_(0, 0.02) for _ in range(copies)]
         fn = lambda i: pkg.gemv(x, ws[i % copies], out=y)  # noqa: E731
         algo = 2 * (N * K + M * K + M * N)
-    ms = timer.per_iter_ms(fn, max(iters, 2 * copies))
+    ms = timer.graph_ms(fn, max(iters, 2 * copies))
     gbs = algo / (ms * 1e-3) / 1e9
     del ws
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
@@ -142,16 +176,18 @@ def bench_gemv(pkg, torch, dev, timer, M, K, N, int8, iters, min_bytes=768 << 20
 
 
 def bench_decode_step(pkg, torch, dev, timer, iters):
-    """One Qwen2.5-0.5B decode step at M=1: 24 layers x (q, k, v, o, gate, up,
-    down) with distinct weights + lm_head, ~0.99 GB streamed."""
+    """One Qwen2.5-0.5B decode step at M=1: 24 layers of distinct weights +
+    lm_head, ~0.99 GB streamed.  Projections that read the same input share
+    one weight matrix (q|k|v 896->1152, gate|up 896->9728), as decoders
+    pack them, so a layer is 4 GEMV launches."""
     H, KV, I, V, L = 896, 128, 4864, 151936, 24
     g = torch.Generator().manual_seed(3)
     x = torch.randn(1, H, generator=g).half().to(dev)
-    shapes = [(H, H), (KV, H), (KV, H), (H, H), (I, H), (I, H), (H, I)]
+    shapes = [(H + 2 * KV, H), (H, H), (2 * I, H), (H, I)]
     layers = [[torch.empty(n, k, dtype=torch.float16, device=dev).normal_(0, 0.02) for n, k in shapes]
               for _ in range(L)]
     lm = torch.empty(V, H, dtype=torch.float16, device=dev).normal_(0, 0.02)
-    outs = {n: torch.empty(1, n, dtype=torch.float16, device=dev) for n in (H, KV, I, V)}
+    outs = {n: torch.empty(1, n, dtype=torch.float16, device=dev) for n in (H, H + 2 * KV, 2 * I, V)}
     xi = torch.randn(1, I, generator=g).half().to(dev)
 
     def step(_i=0):
@@ -162,11 +198,11 @@ def bench_decode_step(pkg, torch, dev, timer, iters):
         pkg.gemv(x, lm, out=outs[V])
 
     nbytes = sum(2 * (w.numel() + w.shape[1] + w.shape[0]) for ws in layers for w in ws) + 2 * (lm.numel() + H + V)
-    ms = timer.per_iter_ms(step, iters, warmup=2)
+    ms = timer.graph_ms(step, iters)
     gbs = nbytes / (ms * 1e-3) / 1e9
     del layers, lm
     return {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-            "bytes": nbytes, "launches": L * 7 + 1}
+            "bytes": nbytes, "launches": L * len(shapes) + 1}
 
 
 def bench_rows(pkg, torch, dev, timer, iters):
@@ -177,12 +213,12 @@ def bench_rows(pkg, torch, dev, timer, iters):
     xs = [torch.randn(rows, cols, generator=g).half().to(dev) for _ in range(copies)]
     w = torch.ones(cols, dtype=torch.float16, device=dev)
     y = torch.empty(rows, cols, dtype=torch.float16, device=dev)
-    ms = timer.per_iter_ms(lambda i: pkg.rms_norm(xs[i % copies], w, 1e-5, out=y), iters)
+    ms = timer.graph_ms(lambda i: pkg.rms_norm(xs[i % copies], w, 1e-5, out=y), iters)
     nb = 2 * (2 * rows * cols + cols)
     out["rmsnorm_512x2048"] = {"us": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)}
     s = torch.randn(96 * 197, 197, generator=g).half().to(dev)
     p = torch.empty_like(s)
-    ms = timer.per_iter_ms(lambda i: pkg.softmax(s, 0.125, out=p), iters)
+    ms = timer.graph_ms(lambda i: pkg.softmax(s, 0.125, out=p), iters)
     nb = 2 * 2 * s.numel()
     out["softmax_18912x197"] = {"us": round(ms * 1e3, 2), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                                 "frac_hbm_peak": round(nb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
@@ -206,7 +242,7 @@ def bench_vit(pkg, torch, dev, timer, iters):
         h = pkg.linear(x, w1, b1, epilogue="gelu_tanh")
         pkg.linear(h, w2, b2)
 
-    ms = timer.per_iter_ms(step, iters)
+    ms = timer.graph_ms(step, iters)
     flops = 2 * (2 * B * Hh * S * S * D) + 2 * (2 * B * S * E * F)
     return {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
 
@@ -271,6 +307,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--profile", action="store_true",
+                    help="for rocprofv3: run only the dominant kernel (gate/up SiLU-mul GEMM) --steps times, then a "
+                         "256 MiB device copy 5 times (calibrates FETCH_SIZE/WRITE_SIZE), and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -287,6 +326,21 @@ def main() -> int:
     timer = Timer(torch)
 
     step, gate_up, _, _ = make_block(pkg, torch, dev)
+    fl = tinyllama_flops()
+    if args.profile:
+        step()
+        for _ in range(args.steps):
+            gate_up()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] profile mode: {args.steps} gate/up launches, 5 x 256 MiB copies")
+        return 0
+    # One step = the block's kernels launched eagerly on torch's current
+    # stream (each kernel outlasts its host launch, so launches queue ahead of
+    # the GPU); HIP events bracket exactly K steps after W warm-up steps.
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -297,15 +351,19 @@ def main() -> int:
     e.record()
     torch.cuda.synchronize()
     ms = s.elapsed_time(e) / args.steps
-    fl = tinyllama_flops()
     value = fl["total"] / (ms * 1e-3) / 1e12
     log(f"[bench] tinyllama block {ms * 1e3:.1f} us/step, {value:.1f} TFLOP/s")
+    graph_step_ms = timer.graph_ms(step, 10)
+    log(f"[bench] tinyllama block as a HIP graph (10 steps per graph) {graph_step_ms * 1e3:.1f} us/step")
 
+    # the dominant kernel alone, back to back on the same stream: its average
+    # launch duration (rocprofv3 kernel-trace of this command agrees)
     gu_ms = timer.per_iter_ms(gate_up, max(args.steps, 20))
     gu_tf = fl["gate_up"] / (gu_ms * 1e-3) / 1e12
     log(f"[bench] gate/up SiLU-mul GEMM {gu_ms * 1e3:.2f} us, {gu_tf:.1f} TFLOP/s")
 
-    secondary = {}
+    secondary = {"tinyllama_block_hip_graph": {"us": round(graph_step_ms * 1e3, 1),
+                                               "tflops": round(fl["total"] / (graph_step_ms * 1e-3) / 1e12, 1)}}
     if not args.quick:
         secondary["gemm_1024_nn"] = bench_gemm(pkg, torch, dev, timer, 1024, 1024, 1024, "nn", 200)
         secondary["gemm_4096_nn"] = bench_gemm(pkg, torch, dev, timer, 4096, 4096, 4096, "nn", 30)
@@ -349,7 +407,7 @@ def main() -> int:
         "config": {"workload": "TinyLlama-1.1B prefill block, 512 tokens, fp16: RMSNorm 2048 -> QKV 2048x2560 -> "
                                "O 2048x2048 -> gate/up 2048x11264 + SiLU-mul -> down 5632x2048",
                    "tokens": TL_M, "hidden": TL_H, "gemm_flop_per_step": fl["total"]},
-        "roofline": {"kernel": "gemm_mfma<128x256> gate/up + SiLU-mul (M=512, N=11264, K=2048)",
+        "roofline": {"kernel": "gemm_mfma, gate/up + SiLU-mul epilogue (M=512, N=11264, K=2048)",
                      "bound": "mfma", "achieved": round(gu_tf, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gu_tf / PEAK_FP16_TFLOPS, 4), "traffic": traffic_from_profiles(),
                      "algorithmic_flop_per_launch": fl["gate_up"], "avg_launch_us": round(gu_ms * 1e3, 3)},

@@ -1,0 +1,161 @@
+"""Drop-in launcher for PyTorch programs, with the reference's entry point
+``TorchMLIRHexagonLauncher().run_torch_mlir(...)``
+(qcom_hexagon_backend/backend/torch_mlir_hexagon_launcher.py:258-306).
+
+Reference flow: model -> torch-mlir linalg bytecode file -> compile to a
+Hexagon .so -> run on the DSP over adb -> output files -> CPU tensors.
+Here: model -> ``export_program`` / ``write_program_to_file`` (a
+torch.export program file takes the place of the linalg bytecode) ->
+``compile_torch_mlir`` plans the graph onto the hxmi kernels
+(backend/graph.py) -> run in-process on the GPU -> CPU tensors.  Same
+arguments, same return value (one CPU tensor per returned tensor), same
+Test_Info report and timestamped artifact folder.
+"""
+from __future__ import annotations
+
+import json
+import os
+import shutil
+import time
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from .graph import Plan, plan_program
+from .hexagon_launcher_base import HexagonLauncherBase, create_timestamped_folder
+from .hexagon_options import HexagonOptions, options_from_dict
+from .utils import write_output_tensor
+
+
+def export_program(model: torch.nn.Module, inputs: Sequence, func_name: str = "main"):
+    """Export `model` for `inputs` (the place of the reference scripts'
+    ``fx_mlir.export_and_import(..., output_type="linalg-on-tensors")``,
+    e.g. benchmark_models/run_tinyllama.py:70-88)."""
+    del func_name  # the program file has one entry, named by the caller at run time
+    model = model.eval()
+    return torch.export.export(model, tuple(inputs))
+
+
+def write_program_to_file(program, filename: str) -> None:
+    """Save an exported program (the place of writing the MLIR bytecode file,
+    benchmark_models/micro_bench/test_matmul_benchmark.py:43-47)."""
+    torch.export.save(program, filename)
+
+
+def _flatten(out):
+    if isinstance(out, torch.Tensor):
+        return [out]
+    if isinstance(out, (list, tuple)):
+        res = []
+        for o in out:
+            res += _flatten(o)
+        return res
+    return []
+
+
+class TorchMLIRHexagonLauncher(HexagonLauncherBase):
+    def __init__(self, device: Optional[torch.device] = None):
+        self.device = device or torch.device("cuda", torch.cuda.current_device() if torch.cuda.is_available() else 0)
+        self.last_plan: Optional[Plan] = None
+
+    def compile_torch_mlir(self, local_dir: str, mlir_bytecode_path: str, func_name: str, options: dict) -> Plan:
+        """Load the program file and plan it onto the GPU kernels; the plan
+        summary is written to <func_name>.plan.txt in the artifact folder."""
+        opts = options_from_dict(options)
+        program = torch.export.load(mlir_bytecode_path)
+        if opts.tileSizes:
+            os.environ["HXMI_GEMM_TILE"] = str(_tile_id(opts.tileSizes))
+        plan = plan_program(program, self.device, fusion=opts.fusion)
+        with open(os.path.join(local_dir, f"{func_name}.plan.txt"), "w") as f:
+            f.write(plan.summary() + "\n")
+        self.last_plan = plan
+        return plan
+
+    def run_torch_mlir(
+        self,
+        mlir_bytecode_path: str,
+        inputs: list[Tensor],
+        func_name: str,
+        base_dir_for_artifacts: Optional[str] = None,
+        iterations: int = 1,
+        options: dict = None,
+        enable_etm=False,
+    ) -> list[Tensor]:
+        if options is None:
+            options = HexagonOptions().__dict__
+        opts = options_from_dict(options)
+        if enable_etm:
+            raise NotImplementedError("ETM tracing has no MI355X equivalent; profile with rocprofv3")
+        local_dir = create_timestamped_folder(func_name, base_dir_for_artifacts)
+        shutil.copy(mlir_bytecode_path, os.path.join(local_dir, os.path.basename(mlir_bytecode_path)))
+
+        start = time.time()
+        plan = self.compile_torch_mlir(local_dir, mlir_bytecode_path, func_name, options)
+        print(f"Compilation from program file to GPU plan took {time.time() - start:.4f} seconds", flush=True)
+        return self.execute_kernel(plan, inputs, func_name, local_dir, iterations, opts.enableLWP)
+
+    def execute_kernel(self, plan: Plan, inputs: list, func_name: str, local_dir: str, iterations: int = 1,
+                       lwp: bool = False) -> list[Tensor]:
+        """Run the plan on the GPU: one untimed run, `iterations` timed runs
+        (HIP events), the Test_Info report, outputs as CPU tensors (also
+        written to <func_name>_o<i>.raw in the reference's output format)."""
+        args = [x.to(self.device) if isinstance(x, torch.Tensor) else x for x in inputs]
+        gm = plan.module
+        with torch.no_grad():
+            outs = gm(*args)
+            torch.cuda.synchronize(self.device)
+            iters = max(int(iterations), 1)
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(iters):
+                outs = gm(*args)
+            e.record()
+            torch.cuda.synchronize(self.device)
+        self.report(local_dir, "_mlir_ciface_" + func_name, s.elapsed_time(e) * 1e3 / iters)
+        if lwp:
+            self._per_op_timing(plan, args, local_dir)
+        results = [o.detach().cpu() for o in _flatten(outs)]
+        for i, r in enumerate(results):
+            try:
+                write_output_tensor(os.path.join(local_dir, f"_mlir_ciface_{func_name}_o{i}.raw"), r)
+            except ValueError:
+                pass  # dtype without a raw-file id (e.g. bool): returned, not written
+        return results
+
+    def _per_op_timing(self, plan: Plan, args: list, local_dir: str) -> None:
+        """GPU time of every node (HIP events around it), as lwp.json."""
+        from torch.fx import Interpreter
+
+        times = []
+
+        class Timed(Interpreter):
+            def run_node(self, n):
+                if n.op not in ("call_function", "call_module"):
+                    return super().run_node(n)
+                s = torch.cuda.Event(enable_timing=True)
+                e = torch.cuda.Event(enable_timing=True)
+                s.record()
+                r = super().run_node(n)
+                e.record()
+                times.append((n, s, e))
+                return r
+
+        with torch.no_grad():
+            Timed(plan.module).run(*args)
+        torch.cuda.synchronize(self.device)
+        rows = [{"node": n.name, "target": str(n.target), "us": round(s.elapsed_time(e) * 1e3, 3)}
+                for n, s, e in times]
+        with open(os.path.join(local_dir, "lwp.json"), "w") as f:
+            json.dump(rows, f, indent=1)
+
+
+def _tile_id(tile_sizes: str) -> int:
+    """'BM,BN' -> the GEMM tile id with that shape."""
+    shapes = {(256, 256): 8, (128, 256): 1, (256, 128): 2, (128, 128): 3, (64, 128): 4, (128, 64): 5, (64, 64): 6}
+    try:
+        bm, bn = (int(v) for v in tile_sizes.replace("x", ",").split(",")[:2])
+        return shapes[(bm, bn)]
+    except (ValueError, KeyError):
+        raise ValueError(f"tileSizes {tile_sizes!r}: expected 'BM,BN' among {sorted(shapes)}") from None

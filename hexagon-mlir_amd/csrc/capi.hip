@@ -37,7 +37,8 @@ int from_hip(hipError_t e, const char* what) {
 
 int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M,
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC,
-                int b_is_nt, int epilogue, float alpha, int out_f32, void* stream, const char* name) {
+                int b_is_nt, int epilogue, float alpha, int out_f32, void* ws, int64_t ws_bytes, void* stream,
+                const char* name) {
   REQUIRE(batch >= 0 && M >= 0 && N >= 0 && K >= 0, "%s: negative size (batch=%lld M=%lld N=%lld K=%lld)", name,
           (long long)batch, (long long)M, (long long)N, (long long)K);
   REQUIRE(b_is_nt == 0 || b_is_nt == 1, "%s: b_is_nt must be 0 or 1", name);
@@ -74,6 +75,8 @@ int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bi
   p.epilogue = epilogue;
   p.out_f32 = out_f32;
   p.tile = -1;
+  p.ws = ws_bytes > 0 ? ws : nullptr;
+  p.ws_bytes = ws_bytes > 0 ? ws_bytes : 0;
   return from_hip(hxmi::launch_gemm(p, (hipStream_t)stream), name);
 }
 
@@ -110,29 +113,51 @@ const char* hxmi_last_error(void) { return g_err; }
 int hxmi_version(void) { return 100; }
 
 int hxmi_gemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
-                  int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream) {
+                  int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
   return gemm_common(hxmi::DT_F16, A, B, C, bias, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, b_is_nt, epilogue, alpha, 0,
-                     stream, "hxmi_gemm_f16");
+                     workspace, workspace_bytes, stream, "hxmi_gemm_f16");
 }
 
 int hxmi_gemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
-                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream) {
+                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
   return gemm_common(hxmi::DT_BF16, A, B, C, bias, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, b_is_nt, epilogue, alpha, 0,
-                     stream, "hxmi_gemm_bf16");
+                     workspace, workspace_bytes, stream, "hxmi_gemm_bf16");
+}
+
+int64_t hxmi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_is_nt, int epilogue) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  hxmi::GemmProblem p{};
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  // a contiguous, 16-byte aligned stand-in: the split decision depends on
+  // shapes only, the fast-path check needs some aligned address
+  p.A = p.B = p.C = (void*)(uintptr_t)256;
+  p.lda = K;
+  p.ldb = b_is_nt ? K : N;
+  p.ldc = epilogue == HXMI_EPI_SILU_MUL ? N / 2 : N;
+  p.batch = 1;
+  p.b_nt = b_is_nt;
+  p.epilogue = epilogue;
+  p.dtype = hxmi::DT_F16;
+  p.tile = -1;
+  return hxmi::gemm_workspace_bytes(p);
 }
 
 int hxmi_bgemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M, int64_t N,
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
                    int64_t strideC, int b_is_nt, int epilogue, float alpha, void* stream) {
   return gemm_common(hxmi::DT_F16, A, B, C, bias, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, b_is_nt,
-                     epilogue, alpha, 0, stream, "hxmi_bgemm_f16");
+                     epilogue, alpha, 0, nullptr, 0, stream, "hxmi_bgemm_f16");
 }
 
 int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M, int64_t N,
                     int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
                     int64_t strideC, int b_is_nt, int epilogue, float alpha, void* stream) {
   return gemm_common(hxmi::DT_BF16, A, B, C, bias, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, b_is_nt,
-                     epilogue, alpha, 0, stream, "hxmi_bgemm_bf16");
+                     epilogue, alpha, 0, nullptr, 0, stream, "hxmi_bgemm_bf16");
 }
 
 int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
@@ -147,7 +172,7 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
                        16 * ldx * 2 < (1ll << 31);
   if (!gemv_ok)
     return gemm_common(hxmi::DT_F16, x, W, y, bias, 1, M, N, K, ldx, ldw, ldy, 0, 0, 0, 1,
-                       bias ? HXMI_EPI_BIAS : HXMI_EPI_NONE, 1.f, 0, stream, name);
+                       bias ? HXMI_EPI_BIAS : HXMI_EPI_NONE, 1.f, 0, nullptr, 0, stream, name);
   hxmi::GemvProblem p{};
   p.x = x;
   p.W = W;
@@ -164,7 +189,8 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
 }
 
 int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const void* bias, void* y, int64_t M,
-                    int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* stream) {
+                    int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
   const char* name = "hxmi_gemv_w8a16";
   REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", name);
   if (M == 0 || N == 0) return ok();
@@ -190,7 +216,23 @@ int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const vo
   p.w_int8 = 1;
   if (M <= 16) return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
   REQUIRE(N % 8 == 0, "%s: M > 16 needs N %% 8 == 0", name);
-  return from_hip(hxmi::launch_w8a16_gemm(p, (hipStream_t)stream), name);
+  return from_hip(hxmi::launch_w8a16_gemm(p, workspace_bytes > 0 ? workspace : nullptr,
+                                          workspace_bytes > 0 ? workspace_bytes : 0, (hipStream_t)stream),
+                  name);
+}
+
+int64_t hxmi_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 16 || N <= 0 || K <= 0) return 0;
+  hxmi::GemvProblem g{};
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.ldx = K;
+  g.ldw = K;
+  g.ldy = N;
+  g.x = g.W = g.y = (void*)(uintptr_t)256;
+  g.w_int8 = 1;
+  return hxmi::gemm_workspace_bytes(hxmi::w8a16_as_gemm(g));
 }
 
 int hxmi_rmsnorm_f16(const void* x, const void* g, void* y, int64_t rows, int64_t cols, int64_t ldx, int64_t ldy,
@@ -217,7 +259,7 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
 int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,
                             const hxmi_f16_t* inW) {
   const int rc = gemm_common(hxmi::DT_F16, inAct, inW, outM, nullptr, 1, n_row, n_col, n_inner, n_inner, n_col, n_col,
-                             0, 0, 0, 0, HXMI_EPI_NONE, 1.f, 1, nullptr, "hexkl_matmul_f16f16_f32");
+                             0, 0, 0, 0, HXMI_EPI_NONE, 1.f, 1, nullptr, 0, nullptr, "hexkl_matmul_f16f16_f32");
   if (rc != HXMI_OK) return rc;
   return from_hip(hipStreamSynchronize(nullptr), "hexkl_matmul_f16f16_f32");
 }

@@ -41,6 +41,7 @@ struct KArgs {
   float alpha;
   int tiles_m, tiles_n;
   int group_m;
+  int k_last;  // > 0: the last batch entry has this K (split-K: a ragged last slice)
 };
 
 template <typename T>
@@ -82,19 +83,30 @@ __device__ __forceinline__ void map_tile(int bid, const KArgs& a, int& b, int& t
   tn = wi / gsz;
 }
 
-// A k-contiguous tile is stored as [rows][64 elements]: 128-byte rows, two
-// rows per 256-byte line of the 64 4-byte LDS banks.  A ds_read_b128 phase
-// serves 16 lanes, which read the same 16-byte chunk of 16 consecutive rows;
-// XOR-ing the chunk index with (row >> 1) & 7 puts those 16 reads in 16
-// distinct bank groups.
-__device__ __forceinline__ int kc_swz(int r) { return (r >> 1) & 7; }
+// A k-contiguous tile is stored as [rows][BK elements]: RB = 2*BK bytes per
+// row (64 or 128), 256/RB rows per 256-byte line of the 64 4-byte LDS banks.
+// A ds_read_b128 phase serves 16 lanes, which read the same 16-byte chunk of
+// 16 consecutive rows; XOR-ing the chunk index with (row / (256/RB)) mod
+// (RB/16) puts those 16 reads in 16 distinct bank groups.
+template <int RB>
+__device__ __forceinline__ int kc_swz(int r) {
+  return (r / (256 / RB)) & (RB / 16 - 1);
+}
 
 // MFMA 32x32x16 operand layout: lane l holds row (l % 32), k = 8*(l / 32) .. +7
-// of the 16-deep step s.
+// of the 16-deep substep s.
+template <int RB>
 __device__ __forceinline__ short8v read_kc(const char* tile, int r_off, int s, int lane) {
   const int r = r_off + (lane & 31);
   const int c = (s << 1) + (lane >> 5);
-  return *(const short8v*)(tile + r * 128 + ((c ^ kc_swz(r)) << 4));
+  return *(const short8v*)(tile + r * RB + ((c ^ kc_swz<RB>(r)) << 4));
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
 template <int BN>
@@ -188,20 +200,27 @@ __device__ __forceinline__ void schedule_substep() {
   });
 }
 
-template <int BM, int BN, int WM, int WN, bool NN, typename T, int EPI, bool OUTF32, bool BI8 = false>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool NN, typename T, int EPI, bool OUTF32,
+          bool BI8 = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_BYTES = BM * BK * 2;
-  constexpr int B_BYTES = BN * BK * 2;
+  constexpr int RB = BK * 2;            // bytes per k-contiguous tile row
+  constexpr int CH = RB / 16;           // 16-byte chunks per row
+  constexpr int RPIK = 1024 / RB;       // k-contiguous rows per 1 KB wave instruction
+  constexpr int A_BYTES = BM * RB;
+  constexpr int B_BYTES = BN * RB;
   constexpr int STAGE = A_BYTES + B_BYTES;
   constexpr int BNO = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int SROW = BNO * 2 + 16;
   constexpr int EPI_BYTES = OUTF32 ? 0 : BM * SROW;
-  constexpr int SMEM = (2 * STAGE > EPI_BYTES) ? 2 * STAGE : EPI_BYTES;
-  static_assert(BM % (8 * NW) == 0, "A tile rows per wave");
-  static_assert(NN || BN % (8 * NW) == 0, "B tile rows per wave");
-  static_assert(!BI8 || (!NN && !OUTF32), "int8 B is [N,K] with fp16 output");
+  constexpr int SMEM = (STAGES * STAGE > EPI_BYTES) ? STAGES * STAGE : EPI_BYTES;
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(STAGES >= 2 && STAGES <= 4, "STAGES");
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(BM % (RPIK * NW) == 0, "A tile rows per wave");
+  static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
+  static_assert(!BI8 || (!NN && STAGES == 2 && BK == 64), "int8 B: [N,K], BK 64, 2 stages");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -211,7 +230,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   int b, tm, tn;
   map_tile(blockIdx.x, a, b, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int K = a.K;
+  const int K = (a.k_last > 0 && b == a.batch - 1) ? a.k_last : a.K;
 
   const char* Ab = a.A + (b * a.sA + (int64_t)m0 * a.lda) * 2;
   const char* Bb = NN    ? a.B + (b * a.sB + (int64_t)n0) * 2
@@ -219,25 +238,28 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
                          : a.B + (b * a.sB + (int64_t)n0 * a.ldb) * 2;
 
   // ---- load plan --------------------------------------------------------------
-  // Each wave instruction moves 1 KB (8 rows of a k-contiguous tile, or
+  // Each wave instruction moves 1 KB (RPIK rows of a k-contiguous tile, or
   // 1024/(2*BN) rows of an NN tile).  One buffer resource per operand and
   // K-step starts at the step's first column and ends (num_records) at the
   // last valid row, so rows past M / N / K read as zero.  The only per-lane
   // state is one byte offset per operand; a chunk past K swaps it for kOOB.
-  constexpr int IA = BM / 8 / NW;
-  // lane l of an instruction fills slot (row (l >> 3), position l & 7) of its
-  // 8-row block, so it loads logical chunk position ^ kc_swz(row); with an even
-  // wave count that only depends on the wave's parity and l >> 4
-  static_assert(NW % 2 == 0, "even wave count");
-  const int cA = (lane & 7) ^ (((w & 1) << 2) | (lane >> 4));
-  const uint32_t voffA = (uint32_t)((w * 8 + (lane >> 3)) * a.lda * 2 + cA * 16);
-  const uint32_t stepA = (uint32_t)(NW * 8 * a.lda * 2);  // bytes between a wave's A instructions
+  //
+  // Lane l of a k-contiguous instruction fills slot (row l / CH, position
+  // l % CH) of its RPIK-row block, so it loads logical chunk
+  // position ^ kc_swz(row); the swizzle term does not depend on which of the
+  // wave's instructions it is (checked below), so one offset serves them all.
+  static_assert(((NW * RPIK) / (256 / RB)) % CH == 0, "swizzle period");
+  constexpr int IA = BM / RPIK / NW;
+  const int cA = (lane % CH) ^ ((((w * RPIK) / (256 / RB)) + (lane / CH) / (256 / RB)) % CH);
+  const uint32_t voffA = (uint32_t)((w * RPIK + lane / CH) * a.lda * 2 + cA * 16);
+  const uint32_t stepA = (uint32_t)(NW * RPIK * a.lda * 2);  // bytes between a wave's A instructions
   const uint32_t bytesA = (uint32_t)(min(BM, a.M - m0) * a.lda * 2);
 
   constexpr int CPR = BN / 8;                          // NN: 16-byte chunks per k-row
-  constexpr int RPI = NN ? (1024 / (BN * 2)) : 8;      // rows per wave instruction
-  constexpr int IB = BI8 ? 1 : (NN ? (BK / RPI / NW) : (BN / 8 / NW));
+  constexpr int RPI = NN ? (1024 / (BN * 2)) : RPIK;   // rows per wave instruction
+  constexpr int IB = BI8 ? 1 : (NN ? (BK / RPI / NW) : (BN / RPIK / NW));
   static_assert(IB >= 1, "B load plan");
+  static_assert(!NN || (NW * RPI) % 4 == 0, "NN swizzle period");
   uint32_t voffB, stepB, bytesB;
   if constexpr (NN) {
     const int rowl = w * RPI + lane / CPR;  // (row & 3) is the same for every instruction
@@ -246,8 +268,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     stepB = (uint32_t)(NW * RPI * a.ldb * 2);
     bytesB = (uint32_t)(a.ldb * 2);  // per valid k-row
   } else {
-    voffB = (uint32_t)((w * 8 + (lane >> 3)) * a.ldb * (BI8 ? 1 : 2) + cA * 16);
-    stepB = (uint32_t)(NW * 8 * a.ldb * 2);
+    voffB = (uint32_t)((w * RPIK + lane / CH) * a.ldb * (BI8 ? 1 : 2) + cA * 16);
+    stepB = (uint32_t)(NW * RPIK * a.ldb * 2);
     bytesB = (uint32_t)(min(BN, a.N - n0) * a.ldb * (BI8 ? 1 : 2));
   }
   const int nk = (K + BK - 1) / BK;
@@ -277,8 +299,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
         const int r = idx >> 2, q = idx & 3;
         const short8v lo = dequant8(int2v{regQ[i][0], regQ[i][1]});
         const short8v hi = dequant8(int2v{regQ[i][2], regQ[i][3]});
-        *(short8v*)(sB_ + r * 128 + (((2 * q) ^ kc_swz(r)) << 4)) = lo;
-        *(short8v*)(sB_ + r * 128 + (((2 * q + 1) ^ kc_swz(r)) << 4)) = hi;
+        *(short8v*)(sB_ + r * RB + (((2 * q) ^ kc_swz<RB>(r)) << 4)) = lo;
+        *(short8v*)(sB_ + r * RB + (((2 * q + 1) ^ kc_swz<RB>(r)) << 4)) = hi;
       }
     }
   };
@@ -316,10 +338,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       if constexpr (NN)
         fb[i] = read_nn<BN>(sB_, wn * WN + i * 32, s, lane);
       else
-        fb[i] = read_kc(sB_, wn * WN + i * 32, s, lane);
+        fb[i] = read_kc<RB>(sB_, wn * WN + i * 32, s, lane);
     }
 #pragma unroll
-    for (int j = 0; j < TM; ++j) fa[j] = read_kc(sA_, wm * WM + j * 32, s, lane);
+    for (int j = 0; j < TM; ++j) fa[j] = read_kc<RB>(sA_, wm * WM + j * 32, s, lane);
   };
 
   float16v acc[TN][TM];
@@ -328,43 +350,45 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = float16v{};
 
-  // Software pipeline over K-steps (two LDS stages, fragments double
-  // buffered in registers).  Per K-step kt, in stage kt&1:
-  //   substeps 0..2: MFMAs of substep s, reads of substep s+1 in between;
-  //   then: wait for step kt+1's loads, barrier (step kt+1 visible; every
-  //   wave has read all of step kt), refill stage kt&1 with step kt+2;
-  //   substep 3: MFMAs, with step kt+1's first fragments and step kt+2's
-  //   global loads in between.
+  // Software pipeline over K-steps: STAGES LDS stages (step kt lives in stage
+  // kt % STAGES), fragments double buffered in registers.  Per K-step kt:
+  //   substeps 0..SUBS-2: MFMAs of substep s, reads of substep s+1 between;
+  //   then: wait until step kt+1 has landed (later steps may still be in
+  //   flight), barrier (step kt+1 visible; every wave has read all of step
+  //   kt), refill step kt's stage with step kt+STAGES;
+  //   last substep: MFMAs, with step kt+1's first fragments and the new
+  //   step's global loads in between.
   constexpr int SUBS = BK / 16;
   constexpr int NDS = (NN ? 2 * TN : TN) + TM;  // LDS read instructions per substep
-  constexpr int NVM = BI8 ? IA : IA + IB;       // global->LDS loads per K-step
-  issue(0, 0);
-  issue(1, 1);
+  constexpr int NVM = BI8 ? IA : IA + IB;       // global->LDS loads per K-step per wave
+#pragma unroll
+  for (int p = 0; p < STAGES; ++p) issue(p, p);
   if constexpr (BI8) {
     load_q(0);
     store_q(0);
     load_q(1);
   }
-  wait_vmcnt0();
+  wait_vmcnt<(STAGES - 1) * NVM>();
   __syncthreads();
   short8v fa[2][TM], fb[2][TN];
   read_frags(fa[0], fb[0], smem, smem + A_BYTES, 0);
+  int st = 0;
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const char* sA_ = smem + cur * STAGE;
+    const int st1 = (st + 1 == STAGES) ? 0 : st + 1;
+    const char* sA_ = smem + st * STAGE;
     const char* sB_ = sA_ + A_BYTES;
     static_for<SUBS>([&](auto S) {
       constexpr int s = decltype(S)::value;
       constexpr int nxt = (s + 1) & 1;
       if constexpr (s + 1 < SUBS) {
         read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1);
-        if constexpr (BI8 && s == 1) store_q(cur ^ 1);
+        if constexpr (BI8 && s == 1) store_q(st1);
       } else {
-        wait_vmcnt0();
+        wait_vmcnt<(STAGES - 2) * NVM>();
         __syncthreads();
-        issue(kt + 2, cur);
+        issue(kt + STAGES, st);
         if constexpr (BI8) load_q(kt + 2);
-        read_frags(fa[nxt], fb[nxt], smem + (cur ^ 1) * STAGE, smem + (cur ^ 1) * STAGE + A_BYTES, 0);
+        read_frags(fa[nxt], fb[nxt], smem + st1 * STAGE, smem + st1 * STAGE + A_BYTES, 0);
       }
 #pragma unroll
       for (int i = 0; i < TN; ++i)
@@ -373,6 +397,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       schedule_substep<TN * TM, NDS, (s + 1 < SUBS) ? 0 : NVM>();
       __builtin_amdgcn_sched_barrier(0);
     });
+    st = st1;
   }
   wait_vmcnt0();
   __syncthreads();
@@ -393,6 +418,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * g + q] * alpha;
+          if constexpr (BI8) {
+            float sv[4];
+            load_bias4<T>(a.scale, n, a.N, sv);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] *= sv[q];
+          }
           if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU_TANH) {
             float bv[4];
             load_bias4<T>(a.bias, n, a.N, bv);
@@ -475,17 +506,21 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 }
 
 struct TileShape {
-  int BM, BN, WM, WN;
+  int BM, BN, WM, WN, BK, STAGES;
 };
 
 constexpr TileShape kTiles[TILE_COUNT] = {
-    {256, 256, 128, 128},  // TILE_256x256
-    {128, 256, 64, 128},   // TILE_128x256
-    {256, 128, 128, 64},   // TILE_256x128
-    {128, 128, 64, 64},    // TILE_128x128
-    {64, 128, 32, 64},     // TILE_64x128
-    {128, 64, 64, 32},     // TILE_128x64
-    {64, 64, 32, 32},      // TILE_64x64
+    {256, 256, 128, 128, 64, 2},  // TILE_256x256
+    {128, 256, 64, 128, 64, 2},   // TILE_128x256
+    {256, 128, 128, 64, 64, 2},   // TILE_256x128
+    {128, 128, 64, 64, 64, 2},    // TILE_128x128
+    {64, 128, 32, 64, 64, 2},     // TILE_64x128
+    {128, 64, 64, 32, 64, 2},     // TILE_128x64
+    {64, 64, 32, 32, 64, 2},      // TILE_64x64
+    {256, 256, 128, 128, 32, 4},  // TILE_256x256_K32S4
+    {256, 256, 128, 64, 64, 2},   // TILE_256x256_W8
+    {128, 128, 64, 64, 32, 4},    // TILE_128x128_K32S4
+    {256, 128, 128, 64, 32, 4},   // TILE_256x128_K32S4
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8>
@@ -493,7 +528,7 @@ hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr TileShape s = kTiles[TILE];
   constexpr int threads = (s.BM / s.WM) * (s.BN / s.WN) * 64;
   const int64_t blocks = (int64_t)k.tiles_m * k.tiles_n * k.batch;
-  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, NN, T, EPI, OUTF32, BI8>),
+  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
 }
@@ -507,6 +542,10 @@ hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
     case TILE_128x128: return launch_one<TILE_128x128, NN, T, EPI, OUTF32, BI8>(k, stream);
     case TILE_64x128: return launch_one<TILE_64x128, NN, T, EPI, OUTF32, BI8>(k, stream);
     case TILE_128x64: return launch_one<TILE_128x64, NN, T, EPI, OUTF32, BI8>(k, stream);
+    case TILE_256x256_K32S4: return launch_one<TILE_256x256_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
+    case TILE_256x256_W8: return launch_one<TILE_256x256_W8, NN, T, EPI, OUTF32, BI8>(k, stream);
+    case TILE_128x128_K32S4: return launch_one<TILE_128x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
+    case TILE_256x128_K32S4: return launch_one<TILE_256x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
     default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8>(k, stream);
   }
 }

@@ -5,7 +5,11 @@
 namespace hxmi {
 namespace gemm {
 
-hipError_t launch_fast_w8(int tile, int epi, const KArgs& k, hipStream_t s) {
+hipError_t launch_fast_w8(int tile, int epi, bool out_f32, const KArgs& k, hipStream_t s) {
+  if (out_f32) {
+    if (epi != EPI_NONE) return hipErrorNotSupported;
+    return launch_tile<false, _Float16, EPI_NONE, true, true>(tile, k, s);
+  }
   switch (epi) {
     case EPI_NONE: return launch_tile<false, _Float16, EPI_NONE, false, true>(tile, k, s);
     case EPI_BIAS: return launch_tile<false, _Float16, EPI_BIAS, false, true>(tile, k, s);

@@ -13,6 +13,8 @@
 //     registers (exact for q in [-128,127]); the per-row scale multiplies the
 //     fp32 sum once, after the K reduction;
 //   * partial sums of the KS waves are reduced through LDS.
+#include <stdlib.h>
+
 #include "hxmi_common.h"
 #include "hxmi_internal.h"
 
@@ -190,16 +192,22 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.ldx = p.ldx;
   v.ldw = p.ldw;
   v.ldy = p.ldy;
-  // Rows per workgroup and K split: aim for >= ~2048 waves in flight so
-  // enough 16-byte loads are outstanding to cover HBM latency.
+  // Rows per workgroup (TPB tiles of 16) and waves splitting K (KS), from a
+  // sweep of every (TPB, KS) on the Qwen2.5-0.5B decode shapes: one 16-row
+  // tile per workgroup keeps the most workgroups in flight for M <= 4; for
+  // M > 4 the x fragments are shared by more rows (TPB 2-4) once there are
+  // enough tiles; 8 waves per workgroup unless a wave would get < 2 K-steps.
   const int64_t tiles16 = (p.N + 15) / 16;
-  int tpb = tiles16 >= 4096 ? 4 : (tiles16 >= 1024 ? 2 : 1);
-  const int64_t blocks = (tiles16 + tpb - 1) / tpb;
-  int ks = 4;
-  while (ks < 16 && blocks * ks < 2048) ks *= 2;
+  int tpb = 1;
+  if (p.M > 4) tpb = tiles16 >= 600 ? 4 : (tiles16 >= 300 ? 2 : 1);
+  if (p.w_int8 && p.M <= 4 && tiles16 >= 4096) tpb = 2;
   const int kstep = p.w_int8 ? 64 : 32;
   const int64_t nsteps = (p.K + kstep - 1) / kstep;
+  int ks = 8;
   while (ks > 4 && nsteps / ks < 2) ks /= 2;
+  // tuning overrides (launch shape only; every shape computes the same sums)
+  if (const char* e = getenv("HXMI_GEMV_TPB")) tpb = atoi(e) == 4 ? 4 : (atoi(e) == 2 ? 2 : 1);
+  if (const char* e = getenv("HXMI_GEMV_KS")) ks = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : 4);
   return p.w_int8 ? launch_sel<true>(tpb, ks, v, stream) : launch_sel<false>(tpb, ks, v, stream);
 }
 

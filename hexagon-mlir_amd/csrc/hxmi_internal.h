@@ -38,10 +38,31 @@ struct GemmProblem {
   int epilogue;  // Epilogue
   int out_f32;   // 1: C is fp32
   int tile;      // forced tile id (< 0: heuristic)
+  void* ws;      // split-K workspace (fp32 partial sums) or null
+  int64_t ws_bytes;
+  const void* scale;  // int8 B only: per-column fp16 scale
 };
 
+// Split-K factor the dispatcher uses for p (1 = none) and the workspace bytes
+// it needs; both depend only on shapes and epilogue.
+int gemm_splits(const GemmProblem& p);
+int64_t gemm_workspace_bytes(const GemmProblem& p);
+
 // Tile shapes the fast kernel is instantiated for.
-enum TileId { TILE_256x256 = 0, TILE_128x256, TILE_256x128, TILE_128x128, TILE_64x128, TILE_128x64, TILE_64x64, TILE_COUNT };
+enum TileId {
+  TILE_256x256 = 0,
+  TILE_128x256,
+  TILE_256x128,
+  TILE_128x128,
+  TILE_64x128,
+  TILE_128x64,
+  TILE_64x64,
+  TILE_256x256_K32S4,
+  TILE_256x256_W8,
+  TILE_128x128_K32S4,
+  TILE_256x128_K32S4,
+  TILE_COUNT
+};
 
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream);
 // Whether p satisfies the alignment rules of the MFMA fast path.
@@ -62,7 +83,8 @@ struct GemvProblem {
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream);
 
 // W8A16 GEMM for larger M (MFMA, int8 weights dequantised in registers).
-hipError_t launch_w8a16_gemm(const GemvProblem& p, hipStream_t stream);
+hipError_t launch_w8a16_gemm(const GemvProblem& p, void* ws, int64_t ws_bytes, hipStream_t stream);
+GemmProblem w8a16_as_gemm(const GemvProblem& p);
 
 struct RowProblem {
   const void* x;

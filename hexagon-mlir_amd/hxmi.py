@@ -32,12 +32,14 @@ _I = ctypes.c_int
 SIGNATURES = {
     "hxmi_last_error": ([], ctypes.c_char_p),
     "hxmi_version": ([], _I),
-    "hxmi_gemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
-    "hxmi_gemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
+    "hxmi_gemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P], _I),
+    "hxmi_gemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P], _I),
+    "hxmi_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
     "hxmi_bgemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_bgemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
-    "hxmi_gemv_w8a16": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_gemv_w8a16": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
+    "hxmi_w8a16_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "hxmi_rmsnorm_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
@@ -78,7 +80,13 @@ def _check(rc: int) -> None:
         raise HxmiError(f"hxmi error {rc}: {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """Handle of torch's current HIP stream on t's device (where it launches)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -114,6 +122,16 @@ def _vec(t: Optional[torch.Tensor], n: int, dtype: torch.dtype, name: str) -> Op
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+def _workspace(nbytes: int, device: torch.device) -> Optional[torch.Tensor]:
+    """Split-K scratch from torch's caching allocator.  The block returns to
+    the allocator when the tensor dies after the launch; the allocator only
+    hands it out again in the order of the stream it was allocated on, so the
+    kernels that use it finish first and concurrent streams never share it."""
+    if nbytes <= 0:
+        return None
+    return torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
 
 
 def gemm(
@@ -156,9 +174,11 @@ def gemm(
     elif out.shape != (M, nout) or out.dtype != a.dtype:
         raise HxmiError(f"out must be {a.dtype} {(M, nout)}")
     ldc = _rowmajor(out, "out")
-    fn = load_library().hxmi_gemm_f16 if a.dtype == torch.float16 else load_library().hxmi_gemm_bf16
+    lib = load_library()
+    ws = _workspace(lib.hxmi_gemm_workspace_bytes(M, N, K, int(nt), EPILOGUES[epilogue]), a.device)
+    fn = lib.hxmi_gemm_f16 if a.dtype == torch.float16 else lib.hxmi_gemm_bf16
     _check(fn(a.data_ptr(), b.data_ptr(), out.data_ptr(), _ptr(bias), M, N, K, lda, ldb, ldc, int(nt),
-              EPILOGUES[epilogue], float(alpha), _stream(a)))
+              EPILOGUES[epilogue], float(alpha), _ptr(ws), 0 if ws is None else ws.numel() * 4, _stream(a)))
     return out
 
 
@@ -267,8 +287,10 @@ def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor, bias: O
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
     ldy = _rowmajor(out, "out")
-    _check(load_library().hxmi_gemv_w8a16(x.data_ptr(), wq.data_ptr(), scale.data_ptr(), _ptr(bias), out.data_ptr(),
-                                          M, N, K, ldx, ldw, ldy, _stream(x)))
+    lib = load_library()
+    ws = _workspace(lib.hxmi_w8a16_workspace_bytes(M, N, K), x.device)
+    _check(lib.hxmi_gemv_w8a16(x.data_ptr(), wq.data_ptr(), scale.data_ptr(), _ptr(bias), out.data_ptr(),
+                               M, N, K, ldx, ldw, ldy, _ptr(ws), 0 if ws is None else ws.numel() * 4, _stream(x)))
     return out
 
 

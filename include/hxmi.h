@@ -62,17 +62,29 @@ int hxmi_version(void);
  * columns [32q, 32q+16) are gate rows 16q..16q+15 and [32q+16, 32q+32) the
  * matching up rows; C receives N/2 columns, C[:, 16q+i] = silu(g_i) * u_i.
  * bias (fp16, N entries) is required for the BIAS epilogues, else ignored.
+ * workspace / workspace_bytes: optional caller-owned device scratch (16-byte
+ * aligned).  When the output has too few tiles to occupy the GPU and K is
+ * long, the GEMM splits K into slices that write fp32 partial sums there and
+ * a second kernel reduces them and applies the epilogue; it needs
+ * hxmi_gemm_workspace_bytes() bytes.  NULL / 0 (or a smaller buffer) runs
+ * the GEMM unsplit.  Two calls must not share a workspace concurrently.
  * Replaces: the linalg.matmul / matmul_transpose_b lowering scheduled by
  * ScheduleMatmulForHVXPass.cpp:69-195 and tiled by VTCMTiling.cpp:231-266
  * (with HexmemCpyToDMA.cpp:120-271 DMA staging), plus the elementwise
  * generics HexagonFusionPass leaves after it (FusionPass.cpp:161-179).
  */
 int hxmi_gemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
-                  int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream);
+                  int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 
 /* Same contract as hxmi_gemm_f16 with bf16 operands, bias and output. */
 int hxmi_gemm_bf16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
-                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* stream);
+                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes a contiguous hxmi_gemm_f16/bf16 call of this shape can use
+ * (0: it never splits K).  Depends on shapes and epilogue only. */
+int64_t hxmi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_is_nt, int epilogue);
 
 /*
  * Strided batched GEMM: for b in [0,batch): C + b*strideC = epilogue(alpha *
@@ -103,11 +115,18 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
  * x, scale, bias, y fp16; Wq int8 [N,K] (symmetric, per-output-channel
  * scale).  Weights are converted to fp16 exactly in registers; the scale
  * multiplies the fp32 sum.  Requires K % 16 == 0, ldw % 16 == 0, N % 4 == 0.
+ * M <= 16 streams Wq once (GEMV kernel); larger M runs the MFMA GEMM with
+ * the int8 operand, which may split K into the optional workspace (see
+ * hxmi_gemm_f16; size from hxmi_w8a16_workspace_bytes).
  * Replaces: no reference kernel (only quant.qcast/dcast lowering to arith,
  * LinalgToLLVMPass.cpp:203-209); defined by the weight-only int8 configs.
  */
 int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const void* bias, void* y, int64_t M,
-                    int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* stream);
+                    int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes a contiguous hxmi_gemv_w8a16 call of this shape can use. */
+int64_t hxmi_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*
  * RMSNorm per row: y = g * T(x * rsqrt(mean(x^2) + eps)), fp32 math, T = fp16

@@ -1,0 +1,224 @@
+"""CPU tests of the reference-compatible Python surface (backend/)."""
+import os
+import re
+import struct
+import types
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import hot_path as ref
+
+
+@pytest.fixture(scope="module")
+def backend(pkg):
+    import hexagon_mlir_amd.backend as b
+
+    return b
+
+
+# ---- HexagonOptions ------------------------------------------------------------------
+
+
+def test_options_defaults_and_validation(backend):
+    o = backend.HexagonOptions()
+    # hot-path flags keep the reference defaults (hexagon_options.py:48-70)
+    assert o.enableVTCMTiling and o.fusion and o.enableVectorization and not o.enableHexKL
+    assert o.iterations == 10 and o.tileSizes == "" and o.target_artifact == "o"
+    with pytest.raises(ValueError, match="Invalid target_artifact"):
+        backend.HexagonOptions(target_artifact="exe")
+    assert backend.HexagonOptions().hash() == backend.HexagonOptions().hash()
+    assert backend.HexagonOptions(fusion=False).hash() != o.hash()
+
+
+def test_options_dict_round_trip(backend):
+    d = backend.HexagonOptions(enableLWP=True).__dict__
+    assert backend.options_from_dict(d).enableLWP
+    d2 = dict(d)
+    d2["enableVTCMTiling"] = False  # callers mutate the dict (run_tinyllama.py:185-198)
+    assert not backend.options_from_dict(d2).enableVTCMTiling
+    with pytest.raises(KeyError, match="notAnOption"):
+        backend.options_from_dict({"notAnOption": 1})
+
+
+# ---- raw tensor files ----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.int8, torch.int32, torch.int64, torch.uint8])
+def test_raw_output_round_trip(backend, tmp_path, dtype):
+    t = (torch.arange(24) - 7).reshape(2, 3, 4).to(dtype)
+    p = tmp_path / "o0.raw"
+    backend.write_output_tensor(p, t)
+    data = p.read_bytes()
+    # tensor.h:232-257: int32 dtype id, int64 rank, int64 shape, data
+    assert struct.unpack_from("<i", data, 0)[0] == backend.DTYPE_IDS[dtype]
+    assert struct.unpack_from("<q", data, 4)[0] == 3
+    assert struct.unpack_from("<3q", data, 12) == (2, 3, 4)
+    assert len(data) == 12 + 24 + 24 * t.element_size()
+    back = backend.read_output_tensor(p)
+    assert back.dtype == dtype and torch.equal(back, t)
+
+
+def test_raw_rank0_and_errors(backend, tmp_path):
+    p = tmp_path / "s.raw"
+    backend.write_output_tensor(p, torch.tensor(3.5))
+    assert backend.read_output_tensor(p).item() == 3.5
+    p.write_bytes(struct.pack("<iq", 2, 1) + struct.pack("<q", 4) + b"\0" * 8)  # 4 floats need 16 bytes
+    with pytest.raises(ValueError, match="data bytes"):
+        backend.read_output_tensor(p)
+    assert backend.to_torch_type(1) == torch.float16 and backend.to_torch_type(4) == torch.int8
+    with pytest.raises(KeyError):
+        backend.to_torch_type(99)
+
+
+def test_raw_input_is_bare_data(backend, tmp_path):
+    t = torch.randn(5, 3).half()
+    p = tmp_path / "t0.raw"
+    backend.write_input_tensor(p, t)
+    assert p.read_bytes() == t.numpy().tobytes()
+
+
+# ---- report and artifact folder ----------------------------------------------------------
+
+
+def test_test_info_parses_like_the_reference(backend):
+    text = backend.format_test_info("_mlir_ciface_mm", 12.5)
+    # benchmark_models/micro_bench/test_matmul_benchmark.py:84-88
+    assert float(re.search(r"Perf:\s*([0-9]+(?:\.[0-9]+)?)", text).group(1)) == 12.5
+    assert re.search(r"Units:\s*([a-zA-Z]+)", text).group(1) == "us"
+    assert "Result:Pass" in text and text.startswith("Test_Info: {")
+
+
+def test_timestamped_folder(backend, tmp_path, monkeypatch):
+    p = backend.create_timestamped_folder("mm", str(tmp_path))
+    assert os.path.isdir(p) and os.path.basename(p).startswith("mm-")
+    monkeypatch.setenv("HEXAGON_MLIR_DUMP_DIR", str(tmp_path))
+    assert os.path.dirname(backend.create_timestamped_folder("x")) == str(tmp_path)
+    with pytest.raises(AssertionError):
+        backend.create_timestamped_folder("x", str(tmp_path / "missing"))
+
+
+# ---- graph planner --------------------------------------------------------------------------
+
+
+class RMS(nn.Module):
+    """HF LlamaRMSNorm forward."""
+
+    def __init__(self, h):
+        super().__init__()
+        self.weight = nn.Parameter(1 + 0.02 * torch.randn(h))
+        self.eps = 1e-5
+
+    def forward(self, x):
+        dt = x.dtype
+        x = x.to(torch.float32)
+        v = x.pow(2).mean(-1, keepdim=True)
+        x = x * torch.rsqrt(v + self.eps)
+        return self.weight * x.to(dt)
+
+
+class Block(nn.Module):
+    def __init__(self, h=64, inter=128):
+        super().__init__()
+        self.norm = RMS(h)
+        self.gate = nn.Linear(h, inter, bias=False)
+        self.up = nn.Linear(h, inter, bias=False)
+        self.down = nn.Linear(inter, h, bias=False)
+        self.fc1 = nn.Linear(h, 96)
+
+    def forward(self, x, q, k, v):
+        hs = self.norm(x)
+        m = self.down(F.silu(self.gate(hs)) * self.up(hs))
+        y = F.gelu(self.fc1(m), approximate="tanh")
+        a = torch.softmax(q @ k.transpose(-1, -2) * 0.125, dim=-1) @ v
+        b = F.scaled_dot_product_attention(q, k, v)
+        return y, a, b, F.rms_norm(x, (x.shape[-1],), self.norm.weight, 1e-5)
+
+
+def block_inputs(seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(4, 64, generator=g).half()
+    q, k, v = (torch.randn(2, 3, 16, 8, generator=g).half() for _ in range(3))
+    return [x, q, k, v]
+
+
+class OraclePkg(types.SimpleNamespace):
+    """Stands in for the kernels on CPU, computing each call with the oracle,
+    so the planner's rewiring (which tensors go where) is checked numerically."""
+
+    @staticmethod
+    def rms_norm(x, w, eps):
+        return torch.from_numpy(ref.rms_norm_hf(x.numpy(), w.detach().numpy(), eps))
+
+    @staticmethod
+    def linear(x, w, b=None, epilogue=None):
+        lead, x2 = x.shape[:-1], x.reshape(-1, x.shape[-1]).numpy()
+        wn, bn = w.detach().numpy(), None if b is None else b.detach().numpy()
+        if epilogue == "silu_mul":
+            y = ref.gemm_epilogue(x2, wn, "nt", "silu_mul")
+        elif epilogue == "gelu_tanh":
+            y = ref.gemm_epilogue(x2, wn, "nt", "gelu_tanh" if bn is None else "bias_gelu_tanh", bn)
+        else:
+            y = ref.linear(x2, wn, bn)
+        return torch.from_numpy(y).half().reshape(*lead, y.shape[-1])
+
+    @staticmethod
+    def attention(q, k, v, scale):
+        return torch.from_numpy(ref.sdpa(q.numpy(), k.numpy(), v.numpy(), scale)).half()
+
+    @staticmethod
+    def pack_gate_up(wg, wu):
+        return torch.from_numpy(ref.pack_gate_up(wg.numpy(), wu.numpy()))
+
+
+def test_planner_matches_hot_path_patterns(backend):
+    torch.manual_seed(0)
+    model = Block().half()
+    ep = backend.export_program(model, block_inputs())
+    plan = backend.plan_program(ep, torch.device("cpu"), fusion=True)
+    pats = sorted(p for p, _ in plan.kernels)
+    assert pats == ["attention", "attention", "linear", "linear_gelu", "rms_norm", "rms_norm", "silu_mul"], pats
+    # nothing of the hot path is left to torch
+    left = " ".join(plan.torch_ops)
+    for op in ("linear", "matmul", "softmax", "rsqrt", "silu", "gelu", "rms_norm", "scaled_dot"):
+        assert op not in left, left
+
+
+def test_planner_without_fusion_keeps_elementwise_ops(backend):
+    torch.manual_seed(0)
+    plan = backend.plan_program(backend.export_program(Block().half(), block_inputs()), torch.device("cpu"),
+                                fusion=False)
+    pats = [p for p, _ in plan.kernels]
+    assert "silu_mul" not in pats and "linear_gelu" not in pats and pats.count("linear") == 4
+    assert any("silu" in t for t in plan.torch_ops) and any("gelu" in t for t in plan.torch_ops)
+
+
+def test_planner_rewiring_is_numerically_right(backend, monkeypatch):
+    torch.manual_seed(0)
+    model = Block().half()
+    inputs = block_inputs(1)
+    from hexagon_mlir_amd.backend import graph
+
+    monkeypatch.setattr(graph, "_pkg", lambda: OraclePkg())
+    plan = backend.plan_program(backend.export_program(model, inputs), torch.device("cpu"), fusion=True)
+    got = plan.module(*inputs)
+    exp = model.float()(*[t.float() for t in inputs])
+    for g, e in zip(got, exp):
+        assert ref.max_err_vs_scale(g.float().numpy(), e.detach().numpy()) < 1e-2
+
+
+def test_planner_leaves_fp32_to_torch(backend):
+    torch.manual_seed(0)
+    model = Block().float()
+    plan = backend.plan_program(backend.export_program(model, [t.float() for t in block_inputs()]),
+                                torch.device("cpu"))
+    assert plan.kernels == []
+
+
+def test_etm_is_not_available(backend, tmp_path):
+    with pytest.raises(NotImplementedError):
+        backend.TorchMLIRHexagonLauncher(torch.device("cpu")).run_torch_mlir(
+            "missing.pt2", [], "f", str(tmp_path), enable_etm=True)

@@ -48,13 +48,13 @@ def test_header_compiles_as_c(tmp_path):
 @pytest.mark.parametrize(
     "args, msg",
     [
-        ((None, None, None, None, -1, 8, 8, 8, 8, 8, 1, 0, 1.0, None), "negative size"),
-        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 2, 0, 1.0, None), "b_is_nt"),
-        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 9, 1.0, None), "unknown epilogue"),
-        ((1, 1, 1, None, 8, 48, 8, 8, 8, 48, 1, 2, 1.0, None), "SiLU-mul"),
-        ((None, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 0, 1.0, None), "null"),
-        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 1, 1.0, None), "bias"),
-        ((1, 1, 1, None, 8, 8, 16, 8, 16, 8, 1, 0, 1.0, None), "leading dimension"),
+        ((None, None, None, None, -1, 8, 8, 8, 8, 8, 1, 0, 1.0, None, 0, None), "negative size"),
+        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 2, 0, 1.0, None, 0, None), "b_is_nt"),
+        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 9, 1.0, None, 0, None), "unknown epilogue"),
+        ((1, 1, 1, None, 8, 48, 8, 8, 8, 48, 1, 2, 1.0, None, 0, None), "SiLU-mul"),
+        ((None, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 0, 1.0, None, 0, None), "null"),
+        ((1, 1, 1, None, 8, 8, 8, 8, 8, 8, 1, 1, 1.0, None, 0, None), "bias"),
+        ((1, 1, 1, None, 8, 8, 16, 8, 16, 8, 1, 0, 1.0, None, 0, None), "leading dimension"),
     ],
 )
 def test_gemm_rejects_invalid_arguments(pkg, args, msg):
@@ -66,7 +66,7 @@ def test_gemm_rejects_invalid_arguments(pkg, args, msg):
 
 def test_empty_problems_are_noops(pkg):
     lib = pkg.load_library()
-    assert lib.hxmi_gemm_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, 1, 0, 1.0, None) == 0
+    assert lib.hxmi_gemm_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, 1, 0, 1.0, None, 0, None) == 0
     assert lib.hxmi_last_error() == b""
     assert lib.hxmi_gemv_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, None) == 0
     assert lib.hxmi_rmsnorm_f16(None, None, None, 0, 16, 16, 16, 1e-5, None) == 0
@@ -82,7 +82,7 @@ def test_row_ops_reject_invalid(pkg):
 
 def test_w8a16_rejects_unaligned_k(pkg):
     lib = pkg.load_library()
-    assert lib.hxmi_gemv_w8a16(16, 16, 16, None, 16, 1, 8, 24, 24, 32, 8, None) == 1
+    assert lib.hxmi_gemv_w8a16(16, 16, 16, None, 16, 1, 8, 24, 24, 32, 8, None, 0, None) == 1
     assert "K % 16" in lib.hxmi_last_error().decode()
 
 
@@ -98,10 +98,22 @@ def test_error_is_thread_local(pkg):
     import threading
 
     lib = pkg.load_library()
-    lib.hxmi_gemm_f16(None, None, None, None, -1, 8, 8, 8, 8, 8, 1, 0, 1.0, None)
+    lib.hxmi_gemm_f16(None, None, None, None, -1, 8, 8, 8, 8, 8, 1, 0, 1.0, None, 0, None)
     seen = []
     t = threading.Thread(target=lambda: seen.append(lib.hxmi_last_error()))
     t.start()
     t.join()
     assert seen == [b""]
     assert lib.hxmi_last_error() != b""
+
+
+def test_workspace_queries(pkg):
+    lib = pkg.load_library()
+    # TinyLlama down projection: 64 tiles of 128x128 -> split K
+    need = lib.hxmi_gemm_workspace_bytes(512, 2048, 5632, 1, 0)
+    assert need > 0 and need % (512 * 2048 * 4) == 0
+    # 4096^3 fills the GPU without splitting; batched / short-K never split
+    assert lib.hxmi_gemm_workspace_bytes(4096, 4096, 4096, 1, 0) == 0
+    assert lib.hxmi_gemm_workspace_bytes(512, 2048, 512, 1, 0) == 0
+    assert lib.hxmi_w8a16_workspace_bytes(16, 896, 4864) == 0  # GEMV path
+    assert lib.hxmi_w8a16_workspace_bytes(256, 896, 4864) > 0

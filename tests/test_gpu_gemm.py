@@ -9,7 +9,7 @@ from oracle import hot_path as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = list(range(7))  # TILE_256x256 .. TILE_64x64
+TILES = list(range(11))  # every instantiated tile shape (TileId)
 
 
 def run_gemm(pkg, dev, a, b, layout, **kw):
@@ -51,7 +51,7 @@ def test_gemm_bias_exact_every_tile(pkg, dev, force_tile, tile):
 @pytest.mark.parametrize("layout", ["nn", "nt"])
 @pytest.mark.parametrize("M,N,K", [(1, 8, 8), (33, 72, 40), (130, 264, 200), (300, 136, 520), (197, 64, 64),
                                    (64, 64, 0), (5, 24, 8)])
-@pytest.mark.parametrize("tile", [None, 0, 3, 6])
+@pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10])
 def test_gemm_ragged_shapes(pkg, dev, force_tile, layout, M, N, K, tile):
     force_tile(tile)
     a = uniform((M, K), 2)
@@ -72,7 +72,7 @@ def test_gemm_unaligned_elementwise_path(pkg, dev, layout, M, N, K, lda):
 
 
 @pytest.mark.parametrize("epi", ["bias", "gelu_tanh", "bias_gelu_tanh"])
-@pytest.mark.parametrize("tile", [None, 0, 3, 6])
+@pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10])
 def test_gemm_epilogues(pkg, dev, force_tile, epi, tile):
     force_tile(tile)
     M, N, K = 300, 264, 256
@@ -167,6 +167,50 @@ def test_bgemm_vit_attention_products(pkg, dev):
     assert ref.max_err_vs_scale(np32(o.cpu()), o_ref) <= TOL
     o_ref_p16 = ref.bmm(np32(p.cpu()), v.numpy())  # same fp16 P: elementwise bound holds
     assert ref.max_rel_err(np32(o.cpu()), o_ref_p16) <= TOL
+
+
+@pytest.fixture
+def force_splits(monkeypatch):
+    def _set(s):
+        if s is None:
+            monkeypatch.delenv("HXMI_SPLITK", raising=False)
+        else:
+            monkeypatch.setenv("HXMI_SPLITK", str(s))
+
+    return _set
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("splits", [2, 3, 4, 8])
+@pytest.mark.parametrize("K", [2048, 2056, 3000 - 3000 % 8])  # even, ragged last slice, odd slice count
+def test_gemm_split_k(pkg, dev, force_splits, layout, splits, K):
+    force_splits(splits)
+    M, N = 200, 264
+    a = uniform((M, K), 30)
+    b = uniform((K, N) if layout == "nn" else (N, K), 31)
+    c = run_gemm(pkg, dev, a, b, layout)
+    assert ref.max_rel_err(np32(c), ref.matmul(a.numpy(), b.numpy(), layout)) <= TOL
+
+
+@pytest.mark.parametrize("epi", ["bias", "gelu_tanh", "bias_gelu_tanh", "silu_mul"])
+def test_gemm_split_k_epilogues(pkg, dev, force_splits, epi):
+    force_splits(4)
+    M, N, K = 130, 320, 4096
+    a = normal((M, K), 32)
+    w = normal((N, K), 33, 0.02)
+    bias = normal((N,), 34, 0.5)
+    c = run_gemm(pkg, dev, a, w, "nt", epilogue=epi, bias=bias.to(dev))
+    exp = ref.gemm_epilogue(a.numpy(), w.numpy(), "nt", epi, bias.numpy())
+    assert ref.max_rel_err(np32(c), exp) <= TOL
+
+
+def test_gemm_split_k_default_down_projection(pkg, dev):
+    # TinyLlama down projection: the dispatcher splits K by itself
+    assert pkg.load_library().hxmi_gemm_workspace_bytes(512, 2048, 5632, 1, 0) > 0
+    x = normal((512, 5632), 35)
+    w = normal((2048, 5632), 36, 0.02)
+    y = run_gemm(pkg, dev, x, w, "nt")
+    assert ref.max_rel_err(np32(y), ref.linear(x.numpy(), w.numpy())) <= TOL
 
 
 def test_hexkl_compat_matmul(pkg, dev):

@@ -1,0 +1,89 @@
+"""GPU end-to-end through the reference-compatible launcher."""
+import re
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from gpu_util import TOL, normal, np32, uniform
+from oracle import hot_path as ref
+from test_backend import Block, block_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+class MatMul(nn.Module):
+    """benchmark_models/micro_bench/test_matmul_benchmark.py:22-31."""
+
+    def __init__(self, transpose_b=False):
+        super().__init__()
+        self.transpose_b = transpose_b
+
+    def forward(self, a, b):
+        if self.transpose_b:
+            b = b.transpose(-2, -1)
+        return torch.matmul(a, b)
+
+
+@pytest.fixture(scope="module")
+def backend(pkg):
+    import hexagon_mlir_amd.backend as b
+
+    return b
+
+
+@pytest.mark.parametrize("transpose_b", [False, True])
+def test_micro_bench_matmul_flow(backend, dev, tmp_path, capsys, transpose_b):
+    a = uniform((1024, 1024), 0)
+    b = uniform((1024, 1024), 1)
+    model = MatMul(transpose_b)
+    path = str(tmp_path / "mm.pt2")
+    backend.write_program_to_file(backend.export_program(model, [a, b]), path)
+    opts = backend.HexagonOptions(enableVTCMTiling=True, enableVectorization=True).__dict__
+    launcher = backend.TorchMLIRHexagonLauncher()
+    out = launcher.run_torch_mlir(path, [a, b], "mm", base_dir_for_artifacts=str(tmp_path), iterations=5,
+                                  options=opts)
+    assert [p for p, _ in launcher.last_plan.kernels] == ["matmul"]
+    text = capsys.readouterr().out
+    perf = float(re.search(r"Perf:\s*([0-9]+(?:\.[0-9]+)?)", text).group(1))
+    assert perf > 0 and re.search(r"Units:\s*([a-zA-Z]+)", text).group(1) == "us"
+    reference = model(a.float(), b.float())
+    # the micro-bench's own check (test_matmul_benchmark.py:91-92)
+    assert torch.allclose(out[0].float(), reference, rtol=1e-3, atol=1e-3)
+    assert ref.max_rel_err(np32(out[0]), reference.numpy()) <= TOL
+
+
+def test_block_through_launcher(backend, dev, tmp_path):
+    torch.manual_seed(0)
+    model = Block().half()
+    inputs = block_inputs(2)
+    path = str(tmp_path / "block.pt2")
+    backend.write_program_to_file(backend.export_program(model, inputs), path)
+    launcher = backend.TorchMLIRHexagonLauncher()
+    opts = backend.HexagonOptions(enableLWP=True).__dict__
+    outs = launcher.run_torch_mlir(path, inputs, "block", str(tmp_path), iterations=2, options=opts)
+    pats = sorted(p for p, _ in launcher.last_plan.kernels)
+    assert pats == ["attention", "attention", "linear", "linear_gelu", "rms_norm", "rms_norm", "silu_mul"]
+    exp = model.float()(*[t.float() for t in inputs])
+    for o, e in zip(outs, exp):
+        assert o.device.type == "cpu" and o.dtype == torch.float16
+        assert ref.max_err_vs_scale(np32(o), e.detach().numpy()) <= TOL
+    folder = next(p for p in tmp_path.iterdir() if p.is_dir() and p.name.startswith("block-"))
+    assert (folder / "lwp.json").exists() and (folder / "perf.txt").exists() and (folder / "block.plan.txt").exists()
+    back = backend.read_output_tensor(folder / "_mlir_ciface_block_o0.raw")
+    assert torch.equal(back, outs[0])
+
+
+def test_fusion_off_gives_same_numbers(backend, dev, tmp_path):
+    torch.manual_seed(0)
+    model = Block().half()
+    inputs = block_inputs(3)
+    path = str(tmp_path / "b.pt2")
+    backend.write_program_to_file(backend.export_program(model, inputs), path)
+    on = backend.TorchMLIRHexagonLauncher().run_torch_mlir(path, inputs, "on", str(tmp_path),
+                                                           options=backend.HexagonOptions(fusion=True).__dict__)
+    off = backend.TorchMLIRHexagonLauncher().run_torch_mlir(path, inputs, "off", str(tmp_path),
+                                                            options=backend.HexagonOptions(fusion=False).__dict__)
+    for a, b in zip(on, off):
+        assert ref.max_err_vs_scale(np32(a), np32(b)) <= TOL
