@@ -256,6 +256,42 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
                     "hxmi_softmax_bf16");
 }
 
+int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q, int64_t s_kv,
+                       int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t stride_q,
+                       int64_t stride_k, int64_t stride_v, int64_t stride_o, float scale, void* stream) {
+  const char* name = "hxmi_attention_f16";
+  REQUIRE(bh >= 0 && s_q >= 0 && s_kv >= 0 && d >= 0, "%s: negative size", name);
+  if (bh == 0 || s_q == 0) return ok();
+  REQUIRE(s_kv > 0, "%s: softmax over zero keys", name);
+  REQUIRE(d == 64 || d == 128, "%s: head dim %lld unsupported (64 or 128)", name, (long long)d);
+  REQUIRE(q && k && v && o, "%s: null pointer", name);
+  REQUIRE(ldq >= d && ldk >= d && ldv >= d && ldo >= d, "%s: leading dimension smaller than head dim", name);
+  REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 && stride_q % 8 == 0 && stride_k % 8 == 0 &&
+              stride_v % 8 == 0 && stride_o % 4 == 0,
+          "%s: strides must keep 16-byte aligned rows", name);
+  REQUIRE(al(q, 16) && al(k, 16) && al(v, 16) && al(o, 8), "%s: q, k, v need 16-byte, o 8-byte alignment", name);
+  REQUIRE(s_q < (1ll << 30) && s_kv < (1ll << 30), "%s: sequence too long", name);
+  hxmi::AttnProblem p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = o;
+  p.bh = bh;
+  p.s = s_q;
+  p.skv = s_kv;
+  p.d = d;
+  p.ldq = ldq;
+  p.ldk = ldk;
+  p.ldv = ldv;
+  p.ldo = ldo;
+  p.sq = stride_q;
+  p.sk = stride_k;
+  p.sv = stride_v;
+  p.so = stride_o;
+  p.scale = scale;
+  return from_hip(hxmi::launch_attention(p, (hipStream_t)stream), name);
+}
+
 int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,
                             const hxmi_f16_t* inW) {
   const int rc = gemm_common(hxmi::DT_F16, inAct, inW, outM, nullptr, 1, n_row, n_col, n_inner, n_inner, n_col, n_col,

@@ -101,10 +101,10 @@ hipError_t launch_softmax(const RowProblem& p, hipStream_t stream);
 
 struct AttnProblem {
   const void* q;  // [B*H, S, D]
-  const void* k;
+  const void* k;  // [B*H, SKV, D]
   const void* v;
   void* o;
-  int64_t bh, s, d;
+  int64_t bh, s, skv, d;
   int64_t sq, sk, sv, so;  // per-(b,h) strides, elements
   int64_t ldq, ldk, ldv, ldo;
   float scale;

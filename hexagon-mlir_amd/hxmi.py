@@ -44,6 +44,7 @@ SIGNATURES = {
     "hxmi_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
+    "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
 }
 
@@ -333,15 +334,30 @@ def softmax(x: torch.Tensor, scale: float = 1.0, out: Optional[torch.Tensor] = N
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
-    """SDPA as the reference lowers it (LowerTmTensor.cpp:91-250):
-    bmm(Q, K^T) * scale -> row softmax -> bmm(P, V); q, k, v are [..., S, D]."""
+    """SDPA as the reference lowers it (LowerTmTensor.cpp:91-250): softmax(scale * Q.K^T) . V over
+    q [..., S, D], k and v [..., S_kv, D].  fp16 with D in {64, 128} runs the fused kernel
+    (hxmi_attention_f16); other cases run the same three steps as bmm(Q, K^T) -> softmax -> bmm(P, V)."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
     lead = q.shape[:-2]
     S, D = q.shape[-2:]
+    if k.shape[-1] != D or k.shape[:-2] != lead or v.shape[:-2] != lead or v.shape[-2] != k.shape[-2]:
+        raise HxmiError(f"attention shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
     q3 = q.reshape(-1, S, D)
     k3 = k.reshape(-1, k.shape[-2], D)
     v3 = v.reshape(-1, v.shape[-2], v.shape[-1])
+    if q.dtype == torch.float16 and D in (64, 128) and v.shape[-1] == D and k.dtype == v.dtype == q.dtype:
+        _require_gpu(q3, k3, v3)
+        q3, k3, v3 = (t if t.stride(-1) == 1 and t.stride(1) % 8 == 0 and t.stride(0) % 8 == 0
+                      and t.data_ptr() % 16 == 0 else t.contiguous() for t in (q3, k3, v3))
+        o = torch.empty((q3.shape[0], S, D), dtype=q.dtype, device=q.device)
+        ldq, bq = _batched(q3, "q")
+        ldk, bk = _batched(k3, "k")
+        ldv, bv = _batched(v3, "v")
+        _check(load_library().hxmi_attention_f16(q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), o.data_ptr(),
+                                                 q3.shape[0], S, k3.shape[1], D, ldq, ldk, ldv, D, bq, bk, bv,
+                                                 S * D, float(scale), _stream(q)))
+        return o.reshape(*lead, S, D)
     s = bgemm(q3, k3, b_layout="nt", alpha=scale)
     p = softmax(s)
     o = bgemm(p, v3, b_layout="nn")

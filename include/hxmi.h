@@ -151,6 +151,21 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
                       void* stream);
 
 /*
+ * Fused attention, fp16: for each of bh (batch x head) slices,
+ *   O[i] = softmax(scale * Q[i] . K^T) . V  over s_kv keys,
+ * Q/O [s_q, d], K/V [s_kv, d] row-major (leading dims ld*, slice strides
+ * stride_*, elements), d = 64 or 128, fp32 softmax and accumulation, no mask.
+ * Replaces: tm_tensor.attention as LowerTmTensor.cpp:52-250 lowers it
+ * (batch_matmul(Q, K^T) -> scale -> softmax -> batch_matmul(P, V), semantics
+ * of qcom_hexagon_backend/test/Conversion/TmTensorToLinalg/SDPA.mlir:18-59)
+ * in one kernel; the same three steps remain available as hxmi_bgemm_f16 +
+ * hxmi_softmax_f16.
+ */
+int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q, int64_t s_kv,
+                       int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t stride_q,
+                       int64_t stride_k, int64_t stride_v, int64_t stride_o, float scale, void* stream);
+
+/*
  * HexKL-compatible matmul: outM[n_row, n_col] (fp32) = inAct[n_row, n_inner]
  * . inW[n_inner, n_col] (both fp16, row-major, contiguous), device pointers,
  * default stream, synchronous like the reference.  Returns 0 on success.
