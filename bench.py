@@ -244,7 +244,12 @@ def bench_vit(pkg, torch, dev, timer, iters):
 
     ms = timer.graph_ms(step, iters)
     flops = 2 * (2 * B * Hh * S * S * D) + 2 * (2 * B * S * E * F)
-    return {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    att_ms = timer.graph_ms(lambda _i=0: pkg.attention(q, k, v, 0.125), iters)
+    att_flops = 2 * (2 * B * Hh * S * S * D)
+    att_bytes = 4 * B * Hh * S * D * 2  # Q, K, V read once, O written once
+    return {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "attention_us": round(att_ms * 1e3, 2), "attention_tflops": round(att_flops / (att_ms * 1e-3) / 1e12, 1),
+            "attention_gbs": round(att_bytes / (att_ms * 1e-3) / 1e9, 1)}
 
 
 def cpu_baseline(budget_s: float = 12.0) -> dict:
