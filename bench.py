@@ -54,14 +54,24 @@ class Timer:
     """HIP events on the stream the kernels are launched on (torch's current
     stream: the C ABI is handed torch.cuda.current_stream())."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, warm_ms: float = 100.0):
         self.torch = torch
+        self.warm_ms = warm_ms
+
+    def _warm(self, fn) -> None:
+        """Back-to-back calls for warm_ms of wall time (steady-state clocks)."""
+        t_end = time.perf_counter() + self.warm_ms * 1e-3
+        while time.perf_counter() < t_end:
+            for i in range(10):
+                fn(i)
+            self.torch.cuda.synchronize()
 
     def per_iter_ms(self, fn, iters: int, warmup: int = 3) -> float:
         """Eager launches (host launch cost included when it dominates)."""
         torch = self.torch
         for _ in range(warmup):
             fn(0)
+        self._warm(fn)
         torch.cuda.synchronize()
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
@@ -94,8 +104,10 @@ class Timer:
         stream the replays run on."""
         torch = self.torch
         g = self.capture(fn, n)
-        g.replay()
-        torch.cuda.synchronize()
+        t_end = time.perf_counter() + self.warm_ms * 1e-3
+        while time.perf_counter() < t_end:
+            g.replay()
+            torch.cuda.synchronize()
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
@@ -310,6 +322,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-ms", type=float, default=300.0,
+                    help="minimum wall time of back-to-back warm-up steps before the timed region")
     ap.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--profile", action="store_true",
@@ -346,9 +360,17 @@ def main() -> int:
     # One step = the block's kernels launched eagerly on torch's current
     # stream (each kernel outlasts its host launch, so launches queue ahead of
     # the GPU); HIP events bracket exactly K steps after W warm-up steps.
+    # Warm-up: at least W steps, and at least --warmup-ms of back-to-back
+    # steps, so the timed steps run at the clocks the GPU settles at under
+    # sustained load (MI355X ramps its clock over tens of milliseconds).
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    t_end = time.perf_counter() + args.warmup_ms * 1e-3
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(args.steps):

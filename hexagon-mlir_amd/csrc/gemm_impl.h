@@ -200,8 +200,23 @@ __device__ __forceinline__ void schedule_substep() {
   });
 }
 
+// Barrier of the ping-pong schedule: nothing is moved across it, and every
+// LDS read of the wave has returned (so no stage is refilled under a reader).
+__device__ __forceinline__ void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt / expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// PP = true: ping-pong schedule for 8 waves in two groups of 4 (group =
+// wave / 4 = the tile's upper or lower half of rows, one wave of each group
+// per SIMD).  The groups run half a K-step apart, separated by workgroup
+// barriers: while one group issues its MFMAs from registers, the other
+// loads its next step's fragments from LDS and issues the global->LDS loads,
+// so every SIMD's MFMA pipe alternates between its two waves.
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool NN, typename T, int EPI, bool OUTF32,
-          bool BI8 = false>
+          bool BI8 = false, bool PP = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -221,6 +236,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(BM % (RPIK * NW) == 0, "A tile rows per wave");
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
   static_assert(!BI8 || (!NN && STAGES == 2 && BK == 64), "int8 B: [N,K], BK 64, 2 stages");
+  static_assert(!PP || (NW == 8 && NWM == 2 && STAGES >= 3 && !BI8), "ping-pong: 2 x 4 waves, >= 3 stages");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -361,6 +377,45 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   constexpr int SUBS = BK / 16;
   constexpr int NDS = (NN ? 2 * TN : TN) + TM;  // LDS read instructions per substep
   constexpr int NVM = BI8 ? IA : IA + IB;       // global->LDS loads per K-step per wave
+  if constexpr (PP) {
+    // Phases alternate memory / compute; group 0 runs phase 2k as the memory
+    // phase of step k and 2k+1 as its compute phase, group 1 one phase later.
+    // The memory phase of step k: issue the loads of step k+D (D = STAGES-1)
+    // into the stage step k-1 used, read all of step k's fragments, wait
+    // until this wave's loads of step k+1 have landed.  A stage is refilled
+    // at phase 2k (group 0) or 2k+1 (group 1); its last reader, group 1's
+    // memory phase of step k-1, ended at phase 2k-1 with its reads returned.
+    // Step k+1 is first read at phase 2k+2, after both groups have waited
+    // for their loads of it (at phases 2k and 2k+1).
+    constexpr int D = STAGES - 1;
+    const int grp = wm;
+#pragma unroll
+    for (int p = 0; p < D; ++p) issue(p, p);
+    wait_vmcnt<(D - 1) * NVM>();
+    __syncthreads();
+    if (grp == 1) pp_barrier();
+    short8v fa[SUBS][TM], fb[SUBS][TN];
+    int st = 0, stw = D;
+    for (int kt = 0; kt < nk; ++kt) {
+      issue(kt + D, stw);
+      const char* sA_ = smem + st * STAGE;
+      const char* sB_ = sA_ + A_BYTES;
+      static_for<SUBS>([&](auto S) { read_frags(fa[decltype(S)::value], fb[decltype(S)::value], sA_, sB_, decltype(S)::value); });
+      wait_vmcnt<(D - 1) * NVM>();
+      pp_barrier();
+      static_for<SUBS>([&](auto S) {
+        constexpr int s = decltype(S)::value;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[s][i], fa[s][j], acc[i][j]);
+      });
+      pp_barrier();
+      st = (st + 1 == STAGES) ? 0 : st + 1;
+      stw = (stw + 1 == STAGES) ? 0 : stw + 1;
+    }
+    if (grp == 0) pp_barrier();
+  } else {
 #pragma unroll
   for (int p = 0; p < STAGES; ++p) issue(p, p);
   if constexpr (BI8) {
@@ -398,6 +453,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       __builtin_amdgcn_sched_barrier(0);
     });
     st = st1;
+  }
   }
   wait_vmcnt0();
   __syncthreads();
@@ -507,6 +563,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 
 struct TileShape {
   int BM, BN, WM, WN, BK, STAGES;
+  bool PP = false;
 };
 
 constexpr TileShape kTiles[TILE_COUNT] = {
@@ -521,6 +578,7 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 256, 128, 64, 64, 2},   // TILE_256x256_W8
     {128, 128, 64, 64, 32, 4},    // TILE_128x128_K32S4
     {256, 128, 128, 64, 32, 4},   // TILE_256x128_K32S4
+    {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8>
@@ -528,7 +586,8 @@ hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr TileShape s = kTiles[TILE];
   constexpr int threads = (s.BM / s.WM) * (s.BN / s.WN) * 64;
   const int64_t blocks = (int64_t)k.tiles_m * k.tiles_n * k.batch;
-  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8>),
+  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8,
+                                (s.PP && !BI8)>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
 }
@@ -546,6 +605,7 @@ hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
     case TILE_256x256_W8: return launch_one<TILE_256x256_W8, NN, T, EPI, OUTF32, BI8>(k, stream);
     case TILE_128x128_K32S4: return launch_one<TILE_128x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
     case TILE_256x128_K32S4: return launch_one<TILE_256x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
+    case TILE_256x256_PP: return launch_one<TILE_256x256_PP, NN, T, EPI, OUTF32, BI8>(k, stream);
     default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8>(k, stream);
   }
 }

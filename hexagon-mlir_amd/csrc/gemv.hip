@@ -13,6 +13,10 @@
 //     registers (exact for q in [-128,127]); the per-row scale multiplies the
 //     fp32 sum once, after the K reduction;
 //   * partial sums of the KS waves are reduced through LDS.
+// The MFMA operand layout makes each wave instruction read 64 bytes of 16
+// rows, half cache lines.  For M <= 8 a second kernel (gemv_valu) uses the
+// vector ALUs instead: a lane load then covers 8 rows x 128 bytes (whole
+// lines), which lets the weights stream with the non-temporal policy.
 #include <stdlib.h>
 
 #include "hxmi_common.h"
@@ -151,6 +155,118 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
   }
 }
 
+// Row-streaming GEMV on the vector ALUs for M <= MM (MM <= 8).  A wave owns
+// groups of 8 weight rows; lane l covers row l / 8 and the 16-byte chunk
+// l % 8 of every 128-byte K-step (8 k for fp16 weights, 16 for int8), so one
+// wave load is 8 rows x 128 contiguous bytes.  x (M x K, zero-padded to whole
+// K-steps) is staged in LDS once per workgroup; the 8 partial dot products of
+// a row are summed with lane shuffles at the end.  Workgroups stride over the
+// row groups so each stages x once.
+template <int MM, bool I8, int U>
+__global__ __launch_bounds__(256) void gemv_valu(VArgs a, int kpad) {
+  constexpr int WPB = 4;
+  constexpr int KC = I8 ? 16 : 8;  // k per lane load
+  constexpr int KSTEP = KC * 8;    // k per wave step
+  extern __shared__ __attribute__((aligned(16))) char xs[];  // [M][kpad] fp16
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 3, c = lane & 7;
+  const int esz = I8 ? 1 : 2;
+  const int M = a.M;
+  const int nsteps = kpad / KSTEP;
+  const int groups = (a.N + 7) / 8;
+
+  // stage x: 16-byte chunks, zero past K
+  const int cpr = kpad / 8;
+  const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
+  for (int i = threadIdx.x; i < M * cpr; i += WPB * 64) {
+    const int m = i / cpr, k = (i % cpr) * 8;
+    *(int4v*)(xs + ((int64_t)m * kpad + k) * 2) = load16(rX, k < a.K ? (uint32_t)((m * a.ldx + k) * 2) : kOOB);
+  }
+  __syncthreads();
+
+  for (int g = blockIdx.x * WPB + w; g < groups; g += gridDim.x * WPB) {
+    const int row = g * 8 + r;
+    const bool rok = row < a.N;
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)g * 8 * a.ldw * esz, 0x7fffffff);
+    const uint32_t wrow = (uint32_t)(r * a.ldw * esz);
+    float acc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[m] = 0.f;
+    for (int s0 = 0; s0 < nsteps; s0 += U) {
+      int4v wv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = (s0 + u) * KSTEP + c * KC;
+        wv[u] = load16_nt(rW, (rok && k < a.K) ? wrow + (uint32_t)(k * esz) : kOOB);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (s0 + u < nsteps) {
+          const int k = (s0 + u) * KSTEP + c * KC;
+          half2v wh[KC / 2];
+          if constexpr (I8) {
+            const short8v lo = dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
+            const short8v hi = dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
+            __builtin_memcpy(&wh[0], &lo, 16);
+            __builtin_memcpy(&wh[4], &hi, 16);
+          } else {
+            __builtin_memcpy(&wh[0], &wv[u], 16);
+          }
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            if (m < M) {
+              half2v xh[KC / 2];
+              const char* xp = xs + ((int64_t)m * kpad + k) * 2;
+              __builtin_memcpy(&xh[0], xp, 16);
+              if constexpr (I8) __builtin_memcpy(&xh[4], xp + 16, 16);
+#pragma unroll
+              for (int q = 0; q < KC / 2; ++q) acc[m] = __builtin_amdgcn_fdot2(wh[q], xh[q], acc[m], false);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      acc[m] += __shfl_xor(acc[m], 1, 64);
+      acc[m] += __shfl_xor(acc[m], 2, 64);
+      acc[m] += __shfl_xor(acc[m], 4, 64);
+    }
+    // lane c writes output row m = c
+    float v = 0.f;
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      if (c == m) v = acc[m];
+    if (rok && c < M) {
+      if (I8) v *= (float)((const _Float16*)a.scale)[row];
+      if (a.bias) v += (float)((const _Float16*)a.bias)[row];
+      ((_Float16*)a.y)[(int64_t)c * a.ldy + row] = (_Float16)v;
+    }
+  }
+}
+
+template <int MM, bool I8>
+hipError_t launch_valu(const VArgs& v, hipStream_t stream) {
+  constexpr int KSTEP = I8 ? 128 : 64;
+  const int kpad = (v.K + KSTEP - 1) / KSTEP * KSTEP;
+  const int groups = (v.N + 7) / 8;
+  int blocks = (groups + 3) / 4;
+  const int cap = 256 * 8;  // enough workgroups to fill every CU several times over
+  if (blocks > cap) blocks = cap;
+  const size_t lds = (size_t)v.M * kpad * 2;
+  hipLaunchKernelGGL((gemv_valu<MM, I8, 8>), dim3(blocks), dim3(256), lds, stream, v, kpad);
+  return hipGetLastError();
+}
+
+template <bool I8>
+hipError_t launch_valu_sel(const VArgs& v, hipStream_t stream) {
+  if (v.M == 1) return launch_valu<1, I8>(v, stream);
+  if (v.M == 2) return launch_valu<2, I8>(v, stream);
+  if (v.M <= 4) return launch_valu<4, I8>(v, stream);
+  return launch_valu<8, I8>(v, stream);
+}
+
 template <int TPB, int KS, bool I8>
 hipError_t launch_cfg(const VArgs& v, hipStream_t stream) {
   constexpr int UNR = TPB >= 4 ? 2 : 4;
@@ -208,6 +324,16 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   // tuning overrides (launch shape only; every shape computes the same sums)
   if (const char* e = getenv("HXMI_GEMV_TPB")) tpb = atoi(e) == 4 ? 4 : (atoi(e) == 2 ? 2 : 1);
   if (const char* e = getenv("HXMI_GEMV_KS")) ks = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : 4);
+  // vector-ALU row streaming: small M, x fits the LDS, enough row groups
+  const int kstep_v = p.w_int8 ? 128 : 64;
+  const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
+  // (measured on the Qwen2.5-0.5B shapes: the row-streaming kernel wins for
+  // long weight matrices -- lm_head -- up to M = 8 (int8: 4) and for M = 1
+  // from N = 4096; the MFMA tiles win where K must be split across waves)
+  const bool fits = p.M <= 8 && p.M * kpad * 2 <= 64 * 1024;
+  bool valu = fits && (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
+  if (const char* e = getenv("HXMI_GEMV_PATH")) valu = (e[0] == 'v') && fits;
+  if (valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
   return p.w_int8 ? launch_sel<true>(tpb, ks, v, stream) : launch_sel<false>(tpb, ks, v, stream);
 }
 

@@ -61,6 +61,7 @@ enum TileId {
   TILE_256x256_W8,
   TILE_128x128_K32S4,
   TILE_256x128_K32S4,
+  TILE_256x256_PP,  // 8 waves, ping-pong schedule
   TILE_COUNT
 };
 

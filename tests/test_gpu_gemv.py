@@ -66,6 +66,56 @@ def test_w8a16_qwen_shapes(pkg, dev, M, K, N):
     assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy())) <= TOL
 
 
+@pytest.fixture
+def gemv_path(monkeypatch):
+    """Force the decode kernel: "mfma" (16-row MFMA tiles) or "valu" (row streaming)."""
+
+    def force(path):
+        monkeypatch.setenv("HXMI_GEMV_PATH", path)
+
+    return force
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("N,K", [(4100, 904), (1028, 136), (8, 64)])
+def test_gemv_both_paths(pkg, dev, gemv_path, path, M, N, K):
+    gemv_path(path)
+    x = normal((M, K), 11 + M)
+    w = normal((N, K), 12, 0.05)
+    b = normal((N,), 13)
+    y = pkg.gemv(x.to(dev), w.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("N,K", [(4104, 912), (264, 144)])
+def test_w8a16_both_paths(pkg, dev, gemv_path, path, M, N, K):
+    gemv_path(path)
+    x = normal((M, K), 21 + M)
+    q, s = int8_weights(N, K, 22)
+    b = normal((N,), 23)
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+def test_w8a16_onehot_exact_both_paths(pkg, dev, gemv_path, path):
+    gemv_path(path)
+    d = np.load(GOLDEN / "w8_onehot.npz")
+    q, cols = torch.from_numpy(d["q"]), d["cols"]
+    M = 5
+    rows = np.resize(np.arange(len(cols)), M)
+    x = torch.zeros((M, q.shape[1]), dtype=torch.float16)
+    x[np.arange(M), cols[rows]] = 1
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), torch.ones(q.shape[0], dtype=torch.float16, device=dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().astype(np.int32), d["y"][rows])
+
+
 @pytest.mark.parametrize("M", [5, 64])
 def test_w8a16_onehot_is_exact(pkg, dev, M):
     # scale 1 and one-hot activations: y must be the int8 weight column itself
