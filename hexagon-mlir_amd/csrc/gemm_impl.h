@@ -236,7 +236,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(BM % (RPIK * NW) == 0, "A tile rows per wave");
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
   static_assert(!BI8 || (!NN && STAGES == 2 && BK == 64), "int8 B: [N,K], BK 64, 2 stages");
-  static_assert(!PP || (NW == 8 && NWM == 2 && !BI8), "ping-pong: 2 x 4 waves");
+  static_assert(!PP || (NW == 8 && NWM == 2 && STAGES >= 3 && !BI8), "ping-pong: 2 x 4 waves, >= 3 stages");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -378,42 +378,31 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   constexpr int NDS = (NN ? 2 * TN : TN) + TM;  // LDS read instructions per substep
   constexpr int NVM = BI8 ? IA : IA + IB;       // global->LDS loads per K-step per wave
   if constexpr (PP) {
-    // Phases alternate; group 0 runs phase 2k as the memory phase of step k
-    // (all of its fragment reads) and 2k+1 as the compute phase, group 1 one
-    // phase later.  Both groups issue the global->LDS loads of step k+D
-    // (D = STAGES-1) in phase 2k: group 0 at the start of its memory phase of
-    // step k, group 1 at the start of its compute phase of step k-1.  They go
-    // into the stage of step k-1, whose readers finished in phases 2k-2
-    // (group 0) and 2k-1 (group 1) with their reads returned.  Step k+1 is
-    // first read in phase 2k+2, so every wave waits for its own loads of it
-    // before the barrier that ends phase 2k+1 (group 0 after its compute
-    // phase, group 1 after its memory phase): loads get 2D phases to land.
+    // Phases alternate memory / compute; group 0 runs phase 2k as the memory
+    // phase of step k and 2k+1 as its compute phase, group 1 one phase later.
+    // The memory phase of step k: issue the loads of step k+D (D = STAGES-1)
+    // into the stage step k-1 used, read all of step k's fragments, wait
+    // until this wave's loads of step k+1 have landed.  A stage is refilled
+    // at phase 2k (group 0) or 2k+1 (group 1); its last reader, group 1's
+    // memory phase of step k-1, ended at phase 2k-1 with its reads returned.
+    // Step k+1 is first read at phase 2k+2, after both groups have waited
+    // for their loads of it (at phases 2k and 2k+1).
     constexpr int D = STAGES - 1;
     const int grp = wm;
 #pragma unroll
     for (int p = 0; p < D; ++p) issue(p, p);
     wait_vmcnt<(D - 1) * NVM>();
     __syncthreads();
-    int nxt = D, stw = D;  // next step to load and its stage
-    auto issue_next = [&]() {
-      issue(nxt, stw);
-      ++nxt;
-      stw = (stw + 1 == STAGES) ? 0 : stw + 1;
-    };
-    if (grp == 1) {
-      issue_next();
-      pp_barrier();
-    }
+    if (grp == 1) pp_barrier();
     short8v fa[SUBS][TM], fb[SUBS][TN];
-    int st = 0;
+    int st = 0, stw = D;
     for (int kt = 0; kt < nk; ++kt) {
-      if (grp == 0) issue_next();
+      issue(kt + D, stw);
       const char* sA_ = smem + st * STAGE;
       const char* sB_ = sA_ + A_BYTES;
       static_for<SUBS>([&](auto S) { read_frags(fa[decltype(S)::value], fb[decltype(S)::value], sA_, sB_, decltype(S)::value); });
-      if (grp == 1) wait_vmcnt<(D - 1) * NVM>();
+      wait_vmcnt<(D - 1) * NVM>();
       pp_barrier();
-      if (grp == 1) issue_next();
       static_for<SUBS>([&](auto S) {
         constexpr int s = decltype(S)::value;
 #pragma unroll
@@ -421,9 +410,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
           for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[s][i], fa[s][j], acc[i][j]);
       });
-      if (grp == 0) wait_vmcnt<(D - 1) * NVM>();
       pp_barrier();
       st = (st + 1 == STAGES) ? 0 : st + 1;
+      stw = (stw + 1 == STAGES) ? 0 : stw + 1;
     }
     if (grp == 0) pp_barrier();
   } else {
@@ -592,7 +581,6 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {128, 128, 64, 64, 32, 4},    // TILE_128x128_K32S4
     {256, 128, 128, 64, 32, 4},   // TILE_256x128_K32S4
     {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
-    {256, 256, 128, 64, 64, 2, true},  // TILE_256x256_PP64
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8>
@@ -620,7 +608,6 @@ hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
     case TILE_128x128_K32S4: return launch_one<TILE_128x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
     case TILE_256x128_K32S4: return launch_one<TILE_256x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
     case TILE_256x256_PP: return launch_one<TILE_256x256_PP, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_256x256_PP64: return launch_one<TILE_256x256_PP64, NN, T, EPI, OUTF32, BI8>(k, stream);
     default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8>(k, stream);
   }
 }

@@ -61,8 +61,7 @@ enum TileId {
   TILE_256x256_W8,
   TILE_128x128_K32S4,
   TILE_256x128_K32S4,
-  TILE_256x256_PP,    // 8 waves, ping-pong schedule, 32-deep K-steps, 3 stages
-  TILE_256x256_PP64,  // the same with 64-deep K-steps, 2 stages
+  TILE_256x256_PP,  // 8 waves, ping-pong schedule, 32-deep K-steps, 3 stages
   TILE_COUNT
 };
 
