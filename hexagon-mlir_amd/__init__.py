@@ -18,6 +18,7 @@ from .hxmi import (
     HxmiNotBuiltError,
     attention,
     bgemm,
+    fold_rms_weight,
     gemm,
     gemv,
     hexkl_matmul,
@@ -25,6 +26,7 @@ from .hxmi import (
     load_library,
     pack_gate_up,
     rms_norm,
+    rms_norm_linear,
     softmax,
     w8a16_linear,
 )
@@ -35,6 +37,7 @@ __all__ = [
     "HxmiNotBuiltError",
     "attention",
     "bgemm",
+    "fold_rms_weight",
     "gemm",
     "gemv",
     "hexkl_matmul",
@@ -42,6 +45,7 @@ __all__ = [
     "load_library",
     "pack_gate_up",
     "rms_norm",
+    "rms_norm_linear",
     "softmax",
     "w8a16_linear",
 ]

@@ -38,7 +38,7 @@ int from_hip(hipError_t e, const char* what) {
 int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M,
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC,
                 int b_is_nt, int epilogue, float alpha, int out_f32, void* ws, int64_t ws_bytes, void* stream,
-                const char* name) {
+                const char* name, int rms = 0, float rms_eps = 0.f) {
   REQUIRE(batch >= 0 && M >= 0 && N >= 0 && K >= 0, "%s: negative size (batch=%lld M=%lld N=%lld K=%lld)", name,
           (long long)batch, (long long)M, (long long)N, (long long)K);
   REQUIRE(b_is_nt == 0 || b_is_nt == 1, "%s: b_is_nt must be 0 or 1", name);
@@ -77,6 +77,8 @@ int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bi
   p.tile = -1;
   p.ws = ws_bytes > 0 ? ws : nullptr;
   p.ws_bytes = ws_bytes > 0 ? ws_bytes : 0;
+  p.rms = rms;
+  p.rms_eps = rms_eps;
   return from_hip(hxmi::launch_gemm(p, (hipStream_t)stream), name);
 }
 
@@ -290,6 +292,27 @@ int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int
   p.so = stride_o;
   p.scale = scale;
   return from_hip(hxmi::launch_attention(p, (hipStream_t)stream), name);
+}
+
+int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                            int64_t ldw, int64_t ldc, int epilogue, float eps, void* stream) {
+  const char* name = "hxmi_rmsnorm_linear_f16";
+  REQUIRE(epilogue == HXMI_EPI_NONE || epilogue == HXMI_EPI_SILU_MUL, "%s: epilogue %d unsupported (none or silu_mul)",
+          name, epilogue);
+  REQUIRE(K > 0 || M <= 0 || N <= 0, "%s: RMSNorm over zero columns", name);
+  REQUIRE(eps >= 0.f, "%s: negative eps", name);
+  return gemm_common(hxmi::DT_F16, x, Wg, C, nullptr, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr,
+                     0, stream, name, 1, eps);
+}
+
+int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+                                 int64_t ldwg, void* stream) {
+  const char* name = "hxmi_fold_rmsnorm_weight_f16";
+  REQUIRE(N >= 0 && K >= 0, "%s: negative size", name);
+  if (N == 0 || K == 0) return ok();
+  REQUIRE(W && g && Wg, "%s: null pointer", name);
+  REQUIRE(ldw >= K && ldwg >= K, "%s: leading dimension smaller than K", name);
+  return from_hip(hxmi::launch_fold_rms_weight(W, g, Wg, N, K, ldw, ldwg, (hipStream_t)stream), name);
 }
 
 int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,

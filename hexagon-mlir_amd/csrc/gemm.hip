@@ -7,7 +7,7 @@
 
 namespace hxmi {
 namespace gemm {
-hipError_t launch_fast_f16(int tile, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s);
+hipError_t launch_fast_f16(int tile, bool nn, int epi, bool out_f32, bool rms, const KArgs& k, hipStream_t s);
 hipError_t launch_fast_bf16(int tile, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s);
 hipError_t launch_fast_w8(int tile, int epi, bool out_f32, const KArgs& k, hipStream_t s);
 
@@ -22,6 +22,8 @@ struct GArgs {
   int64_t lda, ldb, ldc, sA, sB, sC, batch;
   float alpha;
   int nn, epi, out_f32;
+  int rms;  // scale each output row by rsqrt(mean(A[m,:]^2) + rms_eps)
+  float rms_eps;
 };
 
 template <typename T>
@@ -53,6 +55,16 @@ __global__ __launch_bounds__(256) void gemm_elementwise(GArgs a) {
       const float b1 = a.nn ? ld<T>(B, k * a.ldb + c1) : ld<T>(B, c1 * a.ldb + k);
       acc1 += av * b1;
     }
+  }
+  if (a.rms) {
+    float ss = 0.f;
+    for (int64_t k = 0; k < a.K; ++k) {
+      const float av = ld<T>(A, m * a.lda + k);
+      ss += av * av;
+    }
+    const float r = rsqrtf(ss / (float)a.K + a.rms_eps);
+    acc0 *= r;
+    acc1 *= r;
   }
   float v = acc0 * a.alpha;
   if (a.epi == EPI_SILU_MUL) {
@@ -206,14 +218,16 @@ KArgs make_kargs(const GemmProblem& p, int tile) {
   const int gm = env_int("HXMI_GROUP_M", 4);
   k.group_m = gm < 1 ? 1 : (gm > k.tiles_m ? k.tiles_m : gm);
   k.k_last = 0;
+  k.rms_eps = p.rms_eps;
   return k;
 }
 
 hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream_t stream) {
   if ((int64_t)k.tiles_m * k.tiles_n * k.batch >= (1ll << 31)) return hipErrorInvalidValue;
+  if (p.rms && p.dtype != DT_F16) return hipErrorNotSupported;
   if (p.dtype == DT_W8A16) return launch_fast_w8(tile, p.epilogue, p.out_f32, k, stream);
   if (p.dtype == DT_BF16) return launch_fast_bf16(tile, !p.b_nt, p.epilogue, p.out_f32, k, stream);
-  return launch_fast_f16(tile, !p.b_nt, p.epilogue, p.out_f32, k, stream);
+  return launch_fast_f16(tile, !p.b_nt, p.epilogue, p.out_f32, p.rms != 0, k, stream);
 }
 
 }  // namespace
@@ -222,7 +236,7 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 // Split K into slices when the output has too few tiles to occupy the 256
 // CUs and K is long enough that each slice still runs many K-steps.
 int gemm_splits(const GemmProblem& p) {
-  if (p.batch != 1 || p.out_f32 || p.K < 2048 || !gemm_fast_path_ok(p)) return 1;
+  if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || !gemm_fast_path_ok(p)) return 1;
   if (const char* e = getenv("HXMI_SPLITK")) return atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
   // 128x128 output tiles are the unit of work split-K is judged by; below
   // K = 3072 the extra reduction pass costs more than the idle CUs
@@ -263,6 +277,8 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream) {
     g.nn = !p.b_nt;
     g.epi = p.epilogue;
     g.out_f32 = p.out_f32;
+    g.rms = p.rms;
+    g.rms_eps = p.rms_eps;
     const int64_t total = p.batch * p.M * g.Nout;
     const int64_t blocks = (total + 255) / 256;
     if (blocks >= (1ll << 31)) return hipErrorInvalidValue;

@@ -42,6 +42,7 @@ struct KArgs {
   int tiles_m, tiles_n;
   int group_m;
   int k_last;  // > 0: the last batch entry has this K (split-K: a ragged last slice)
+  float rms_eps;  // RMS kernels: epsilon of the row RMSNorm folded into the GEMM
 };
 
 template <typename T>
@@ -182,13 +183,17 @@ __device__ __forceinline__ void static_for(F&& f) {
 // otherwise bunches the LDS reads right before the MFMAs that consume them):
 // the substep's NMF MFMAs with the NDS fragment reads of the next substep
 // and NVM global->LDS loads slotted between them.
-template <int NMF, int NDS, int NVM>
+// NVA vector-ALU instructions (the RMSNorm sums of squares of this substep's
+// fragments) go over the second half of the MFMAs, when every fragment has
+// been consumed once and its LDS read has certainly returned.
+template <int NMF, int NDS, int NVM, int NVA = 0>
 __device__ __forceinline__ void schedule_substep() {
   static_assert(NMF > 0, "substep without MFMAs");
-  constexpr int kMFMA = 0x008, kVMEMR = 0x020, kDSR = 0x100;
+  constexpr int kVALU = 0x002, kMFMA = 0x008, kVMEMR = 0x020, kDSR = 0x100;
   // reads go one per MFMA from the start of the region (they feed the next
   // region); global loads are spread over the slots after them
   constexpr int FREE = NMF > NDS ? NMF - NDS : 1;
+  constexpr int HALF = NMF - NMF / 2;
   static_for<NMF>([&](auto M) {
     constexpr int m = decltype(M)::value;
     __builtin_amdgcn_sched_group_barrier(kMFMA, 1, 0);
@@ -197,6 +202,9 @@ __device__ __forceinline__ void schedule_substep() {
     constexpr int mv = m - (NMF - FREE);
     constexpr int nv = mv >= 0 ? (mv + 1) * NVM / FREE - mv * NVM / FREE : 0;
     if constexpr (nv > 0) __builtin_amdgcn_sched_group_barrier(kVMEMR, nv, 0);
+    constexpr int ma = m - (NMF - HALF);
+    constexpr int na = (NVA > 0 && ma >= 0) ? (ma + 1) * NVA / HALF - ma * NVA / HALF : 0;
+    if constexpr (na > 0) __builtin_amdgcn_sched_group_barrier(kVALU, na, 0);
   });
 }
 
@@ -209,6 +217,12 @@ __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// RMS = true: C = epilogue(rmsnorm(A) . B^T) for an NT GEMM whose B already
+// holds the RMSNorm weight folded in (B[n][k] = g[k] * W[n][k]).  Every wave
+// sums the squares of the A fragments it multiplies (its rows, all of K) and
+// scales its accumulators by rsqrt(mean + eps) before the epilogue, so the
+// normalised activations are never written.
+//
 // PP = true: ping-pong schedule for 8 waves in two groups of 4 (group =
 // wave / 4 = the tile's upper or lower half of rows, one wave of each group
 // per SIMD).  The groups run half a K-step apart, separated by workgroup
@@ -216,7 +230,7 @@ __device__ __forceinline__ void pp_barrier() {
 // loads its next step's fragments from LDS and issues the global->LDS loads,
 // so every SIMD's MFMA pipe alternates between its two waves.
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool NN, typename T, int EPI, bool OUTF32,
-          bool BI8 = false, bool PP = false>
+          bool BI8 = false, bool PP = false, bool RMS = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -237,6 +251,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
   static_assert(!BI8 || (!NN && STAGES == 2 && BK == 64), "int8 B: [N,K], BK 64, 2 stages");
   static_assert(!PP || (NW == 8 && NWM == 2 && STAGES >= 3 && !BI8), "ping-pong: 2 x 4 waves, >= 3 stages");
+  static_assert(!RMS || (!NN && !BI8 && !PP && !OUTF32 && sizeof(T) == 2), "RMSNorm prologue: NT fp16, standard schedule");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -365,6 +380,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   for (int i = 0; i < TN; ++i)
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = float16v{};
+  float ss[TM];  // RMS: this lane's sum of squares of row (j*32 + lane%32), its k half
+#pragma unroll
+  for (int j = 0; j < TM; ++j) ss[j] = 0.f;
 
   // Software pipeline over K-steps: STAGES LDS stages (step kt lives in stage
   // kt % STAGES), fragments double buffered in registers.  Per K-step kt:
@@ -451,7 +469,18 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[s & 1][i], fa[s & 1][j], acc[i][j]);
-      schedule_substep<TN * TM, NDS, (s + 1 < SUBS) ? 0 : NVM>();
+      if constexpr (RMS) {
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+          const half8v h = __builtin_bit_cast(half8v, fa[s & 1][j]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const half2v p2 = {h[2 * q], h[2 * q + 1]};
+            ss[j] = __builtin_amdgcn_fdot2(p2, p2, ss[j], false);
+          }
+        }
+      }
+      schedule_substep<TN * TM, NDS, (s + 1 < SUBS) ? 0 : NVM, RMS ? TM * 4 : 0>();
       __builtin_amdgcn_sched_barrier(0);
     });
     st = st1;
@@ -459,6 +488,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   }
   wait_vmcnt0();
   __syncthreads();
+
+  if constexpr (RMS) {
+    // lanes l and l+32 hold the two k halves of the same row
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const float tot = ss[j] + __shfl_xor(ss[j], 32, 64);
+      const float r = rsqrtf(tot / (float)a.K + a.rms_eps);
+#pragma unroll
+      for (int i = 0; i < TN; ++i) acc[i][j] *= r;
+    }
+  }
 
   // ---- epilogue -------------------------------------------------------------
   const float alpha = a.alpha;
@@ -583,32 +623,32 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
 };
 
-template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8>
+template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false>
 hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr TileShape s = kTiles[TILE];
   constexpr int threads = (s.BM / s.WM) * (s.BN / s.WN) * 64;
   const int64_t blocks = (int64_t)k.tiles_m * k.tiles_n * k.batch;
   hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8,
-                                (s.PP && !BI8)>),
+                                (s.PP && !BI8 && !RMS), RMS>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
 }
 
-template <bool NN, typename T, int EPI, bool OUTF32, bool BI8 = false>
+template <bool NN, typename T, int EPI, bool OUTF32, bool BI8 = false, bool RMS = false>
 hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
   switch (tile) {
-    case TILE_256x256: return launch_one<TILE_256x256, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_128x256: return launch_one<TILE_128x256, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_256x128: return launch_one<TILE_256x128, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_128x128: return launch_one<TILE_128x128, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_64x128: return launch_one<TILE_64x128, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_128x64: return launch_one<TILE_128x64, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_256x256_K32S4: return launch_one<TILE_256x256_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_256x256_W8: return launch_one<TILE_256x256_W8, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_128x128_K32S4: return launch_one<TILE_128x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_256x128_K32S4: return launch_one<TILE_256x128_K32S4, NN, T, EPI, OUTF32, BI8>(k, stream);
-    case TILE_256x256_PP: return launch_one<TILE_256x256_PP, NN, T, EPI, OUTF32, BI8>(k, stream);
-    default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8>(k, stream);
+    case TILE_256x256: return launch_one<TILE_256x256, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_128x256: return launch_one<TILE_128x256, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_256x128: return launch_one<TILE_256x128, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_128x128: return launch_one<TILE_128x128, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_64x128: return launch_one<TILE_64x128, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_128x64: return launch_one<TILE_128x64, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_256x256_K32S4: return launch_one<TILE_256x256_K32S4, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_256x256_W8: return launch_one<TILE_256x256_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_128x128_K32S4: return launch_one<TILE_128x128_K32S4, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_256x128_K32S4: return launch_one<TILE_256x128_K32S4, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_256x256_PP: return launch_one<TILE_256x256_PP, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
   }
 }
 

@@ -41,7 +41,14 @@ struct GemmProblem {
   void* ws;      // split-K workspace (fp32 partial sums) or null
   int64_t ws_bytes;
   const void* scale;  // int8 B only: per-column fp16 scale
+  int rms;            // 1: C = epilogue(rmsnorm(A) . B^T), B holds the folded norm weight
+  float rms_eps;
 };
+
+// Wg[n][k] = fp16(W[n][k] * g[k]): folds an RMSNorm weight into the linear
+// layer that consumes the normalised activations.
+hipError_t launch_fold_rms_weight(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+                                  int64_t ldwg, hipStream_t stream);
 
 // Split-K factor the dispatcher uses for p (1 = none) and the workspace bytes
 // it needs; both depend only on shapes and epilogue.

@@ -45,6 +45,8 @@ SIGNATURES = {
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
+    "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P], _I),
+    "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
 }
 
@@ -250,6 +252,48 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None
     x2 = x.reshape(-1, x.shape[-1])
     y = gemm(x2, w, b_layout="nt", epilogue=epi, bias=bias)
     return y.reshape(*lead, y.shape[-1])
+
+
+def fold_rms_weight(w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """w [N,K] with the RMSNorm weight g [K] folded in: fp16(w[n,k] * g[k]), the
+    weight rms_norm_linear takes (fold a packed gate/up weight after packing)."""
+    _require_gpu(w, g)
+    if w.dtype != torch.float16 or g.dtype != torch.float16:
+        raise HxmiError("fold_rms_weight takes fp16 tensors")
+    if w.dim() != 2:
+        raise HxmiError("fold_rms_weight takes a 2-D weight")
+    N, K = w.shape
+    ldw = _rowmajor(w, "w")
+    g = _vec(g, K, torch.float16, "g")
+    out = torch.empty((N, K), dtype=torch.float16, device=w.device)
+    _check(load_library().hxmi_fold_rmsnorm_weight_f16(w.data_ptr(), g.data_ptr(), out.data_ptr(), N, K, ldw, K,
+                                                       _stream(w)))
+    return out
+
+
+def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, epilogue: Optional[str] = None,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """linear(rms_norm(x, g, eps), w) in one GEMM, with w_folded = fold_rms_weight(w, g);
+    epilogue None or "silu_mul" (w packed by pack_gate_up before folding)."""
+    _require_gpu(x, w_folded, out)
+    if x.dtype != torch.float16 or w_folded.dtype != torch.float16:
+        raise HxmiError("rms_norm_linear takes fp16 tensors")
+    if epilogue not in (None, "silu_mul"):
+        raise HxmiError(f"rms_norm_linear epilogue must be None or 'silu_mul', got {epilogue!r}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    N = w_folded.shape[0]
+    if w_folded.dim() != 2 or w_folded.shape[1] != K:
+        raise HxmiError(f"weight {tuple(w_folded.shape)} does not match x {tuple(x.shape)}")
+    nout = N // 2 if epilogue == "silu_mul" else N
+    if out is None:
+        out = torch.empty((M, nout), dtype=x.dtype, device=x.device)
+    out2 = out.reshape(M, nout)
+    _check(load_library().hxmi_rmsnorm_linear_f16(x2.data_ptr(), w_folded.data_ptr(), out2.data_ptr(), M, N, K,
+                                                  _rowmajor(x2, "x"), _rowmajor(w_folded, "w"), _rowmajor(out2, "out"),
+                                                  EPILOGUES[epilogue], float(eps), _stream(x)))
+    return out2.reshape(*lead, nout)
 
 
 def gemv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,

@@ -151,6 +151,29 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
                       void* stream);
 
 /*
+ * RMSNorm folded into the linear layer that consumes it (LLaMA QKV and
+ * gate/up projections):
+ *   C[M,N'] = epilogue(rmsnorm(x) . W^T),  rmsnorm(x)[m,k] = x[m,k] * g[k] / sqrt(mean_k x[m,k]^2 + eps)
+ * with Wg[N,K] = g (.) W prepared once by hxmi_fold_rmsnorm_weight_f16.  The
+ * row statistics are taken inside the GEMM from the x tiles it multiplies,
+ * so the normalised activations never go to memory.  epilogue: HXMI_EPI_NONE
+ * or HXMI_EPI_SILU_MUL (packed gate/up Wg, as hxmi_gemm_f16; N' = N/2).
+ * fp32 statistics and accumulation; differs from normalise-round-multiply
+ * (HF LlamaRMSNorm) by the fp16 rounding of the normalised activations.
+ * Replaces: the RMSNorm generic chain (SplitReductionUtils.cpp,
+ * TilingPass.cpp:261-289; semantics test/python/triton/test_rms_norm.py:37-63)
+ * plus the matmul_transpose_b after it (ScheduleMatmulForHVXPass.cpp:69-195),
+ * which the reference runs as separate passes over HBM.
+ */
+int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                            int64_t ldw, int64_t ldc, int epilogue, float eps, void* stream);
+
+/* Wg[n,k] = fp16(W[n,k] * g[k]) (fp32 product, one rounding): the weight
+ * hxmi_rmsnorm_linear_f16 takes.  W, Wg [N,K] (leading dims ldw, ldwg), g [K]. */
+int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+                                 int64_t ldwg, void* stream);
+
+/*
  * Fused attention, fp16: for each of bh (batch x head) slices,
  *   O[i] = softmax(scale * Q[i] . K^T) . V  over s_kv keys,
  * Q/O [s_q, d], K/V [s_kv, d] row-major (leading dims ld*, slice strides

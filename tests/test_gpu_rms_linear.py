@@ -1,0 +1,125 @@
+"""GPU parity of RMSNorm folded into the following linear layer
+(hxmi_rmsnorm_linear_f16 + hxmi_fold_rmsnorm_weight_f16).
+
+The fused op computes linear(x / rms(x), Wg) in fp32 with Wg = fp16(g * W):
+the fold is checked bit-exact, the GEMM against the oracle's fp32 RMSNorm
+(test/python/triton/test_rms_norm.py:37-63) applied with the folded weight
+(elementwise max relative error), and the whole against the unfused HF order
+(HF LlamaRMSNorm rounds the normalised activations to fp16 before the
+weight and the linear layer) relative to the output scale: the two differ by
+that fp16 rounding, ~1e-4 absolute."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, normal, np32
+from oracle import hot_path as ref
+
+pytestmark = pytest.mark.gpu
+
+TILES = list(range(12))  # every GEMM tile shape (TileId)
+
+
+def check(y, x, wf_cpu, exp_hf, eps, epi=None):
+    """y against the fp32 oracle on the folded weight (elementwise) and against
+    the unfused HF-order oracle (relative to the output scale)."""
+    xn = ref.rms_norm(x.numpy(), np.ones(x.shape[-1], np.float32), eps)
+    if epi == "silu_mul":
+        wfu = ref.unpack_gate_up_cols(np32(wf_cpu).T, wf_cpu.shape[0])  # gate [K, I], up [K, I]
+        exact = ref.silu_mul_linear(xn, wfu[0].T, wfu[1].T)
+    else:
+        exact = ref.linear(xn, np32(wf_cpu))
+    assert ref.max_rel_err(np32(y), exact) <= TOL
+    assert ref.max_err_vs_scale(np32(y), exp_hf) <= TOL
+
+
+def _norm_weight(K, seed):
+    return (1 + 0.02 * torch.randn(K, generator=torch.Generator().manual_seed(seed))).half()
+
+
+def test_fold_weight_is_one_fp16_rounding(pkg, dev):
+    w = normal((300, 520), 1, 0.02)
+    g = _norm_weight(520, 2)
+    wf = pkg.fold_rms_weight(w.to(dev), g.to(dev)).cpu()
+    exp = (np32(w) * np32(g)[None, :]).astype(np.float16)
+    assert np.array_equal(wf.numpy(), exp)
+
+
+@pytest.mark.parametrize("N,K", [(2560, 2048), (2048, 2048)])  # TinyLlama QKV and O-sized
+def test_rms_norm_linear_tinyllama(pkg, dev, N, K):
+    x = normal((512, K), 3)
+    g = _norm_weight(K, 4)
+    w = normal((N, K), 5, 0.02)
+    wf = pkg.fold_rms_weight(w.to(dev), g.to(dev))
+    y = pkg.rms_norm_linear(x.to(dev), wf, 1e-5).cpu()
+    check(y, x, wf.cpu(), ref.linear(ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-5), w.numpy()), 1e-5)
+
+
+def test_rms_norm_gate_up_silu_mul(pkg, dev):
+    M, I, K = 512, 1408, 2048
+    x = normal((M, K), 6)
+    g = _norm_weight(K, 7)
+    wg = normal((I, K), 8, 0.02)
+    wu = normal((I, K), 9, 0.02)
+    wf = pkg.fold_rms_weight(pkg.pack_gate_up(wg.to(dev), wu.to(dev)), g.to(dev))
+    h = pkg.rms_norm_linear(x.to(dev), wf, 1e-5, epilogue="silu_mul").cpu()
+    xn = ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-5)
+    check(h, x, wf.cpu(), ref.silu_mul_linear(xn, wg.numpy(), wu.numpy()), 1e-5, "silu_mul")
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("epi", [None, "silu_mul"])
+def test_rms_norm_linear_every_tile(pkg, dev, force_tile, tile, epi):
+    force_tile(tile)
+    M, N, K = 200, 320, 264
+    x = normal((M, K), 10)
+    g = _norm_weight(K, 11)
+    if epi is None:
+        w = normal((N, K), 12, 0.05)
+        exp_fn = lambda xn: ref.linear(xn, w.numpy())  # noqa: E731
+        wp = w.to(dev)
+    else:
+        wg, wu = normal((N // 2, K), 13, 0.05), normal((N // 2, K), 14, 0.05)
+        exp_fn = lambda xn: ref.silu_mul_linear(xn, wg.numpy(), wu.numpy())  # noqa: E731
+        wp = pkg.pack_gate_up(wg.to(dev), wu.to(dev))
+    wf = pkg.fold_rms_weight(wp, g.to(dev))
+    y = pkg.rms_norm_linear(x.to(dev), wf, 1e-5, epilogue=epi).cpu()
+    check(y, x, wf.cpu(), exp_fn(ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-5)), 1e-5, epi)
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 40, 45), (33, 72, 1000), (1, 8, 8)])
+def test_rms_norm_linear_ragged_and_unaligned(pkg, dev, M, N, K):
+    # K % 8 != 0 runs the element-wise kernel, which applies the same row scale
+    x = normal((M, K), 15)
+    g = _norm_weight(K, 16)
+    w = normal((N, K), 17, 0.05)
+    wf = pkg.fold_rms_weight(w.to(dev), g.to(dev))
+    y = pkg.rms_norm_linear(x.to(dev), wf, 1e-6).cpu()
+    check(y, x, wf.cpu(), ref.linear(ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-6), w.numpy()), 1e-6)
+
+
+def test_rms_norm_linear_zero_row_and_scale_invariance(pkg, dev):
+    """A zero row stays zero; scaling a row by 4 (exact in fp16) leaves its
+    output unchanged up to eps: the normalisation really is per row."""
+    M, N, K = 64, 256, 512
+    x = normal((M, K), 18)
+    x[5] = 0
+    x4 = x.clone()
+    x4[7] *= 4
+    g = _norm_weight(K, 19)
+    wf = pkg.fold_rms_weight(normal((N, K), 20, 0.05).to(dev), g.to(dev))
+    y = pkg.rms_norm_linear(x.to(dev), wf, 1e-12).cpu()
+    y4 = pkg.rms_norm_linear(x4.to(dev), wf, 1e-12).cpu()
+    assert torch.count_nonzero(y[5]) == 0
+    assert ref.max_rel_err(np32(y4[7]), np32(y[7])) <= 1e-3
+    assert torch.equal(y4[:7], y[:7])
+
+
+def test_rms_norm_linear_rejects_bias_epilogue(pkg, dev):
+    lib = pkg.load_library()
+    t = torch.zeros(64, 64, dtype=torch.float16, device=dev)
+    rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), 64, 64, 64, 64, 64, 64, 1,
+                                     ctypes.c_float(1e-5), None)
+    assert rc == 1 and b"epilogue" in lib.hxmi_last_error()
