@@ -363,16 +363,29 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     }
   };
 
+  // Byte offset of this lane's 16-byte chunk in a k-contiguous fragment of
+  // substep s: the swizzle repeats every 16 rows and fragments start on
+  // multiples of 32 rows, so it depends on the lane alone; the wave's first
+  // row is folded in, leaving a constant per fragment (an immediate offset).
+  constexpr int SUBS_ = BK / 16;
+  uint32_t lofA[SUBS_], lofB[SUBS_];
+#pragma unroll
+  for (int s = 0; s < SUBS_; ++s) {
+    const int l = lane & 31;
+    const uint32_t o = (uint32_t)(l * RB + ((((s << 1) + (lane >> 5)) ^ kc_swz<RB>(l)) << 4));
+    lofA[s] = (uint32_t)(wm * WM * RB) + o;
+    lofB[s] = (uint32_t)(wn * WN * RB) + o;
+  }
   auto read_frags = [&](short8v (&fa)[TM], short8v (&fb)[TN], const char* sA_, const char* sB_, int s) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
       if constexpr (NN)
         fb[i] = read_nn<BN>(sB_, wn * WN + i * 32, s, lane);
       else
-        fb[i] = read_kc<RB>(sB_, wn * WN + i * 32, s, lane);
+        fb[i] = *(const short8v*)(sB_ + lofB[s] + i * 32 * RB);
     }
 #pragma unroll
-    for (int j = 0; j < TM; ++j) fa[j] = read_kc<RB>(sA_, wm * WM + j * 32, s, lane);
+    for (int j = 0; j < TM; ++j) fa[j] = *(const short8v*)(sA_ + lofA[s] + j * 32 * RB);
   };
 
   float16v acc[TN][TM];
