@@ -634,6 +634,8 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {128, 128, 64, 64, 32, 4},    // TILE_128x128_K32S4
     {256, 128, 128, 64, 32, 4},   // TILE_256x128_K32S4
     {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
+    {256, 128, 64, 64, 64, 2},         // TILE_256x128_W8
+    {128, 128, 32, 64, 64, 2},         // TILE_128x128_W8
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false>
@@ -661,6 +663,8 @@ hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
     case TILE_128x128_K32S4: return launch_one<TILE_128x128_K32S4, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     case TILE_256x128_K32S4: return launch_one<TILE_256x128_K32S4, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     case TILE_256x256_PP: return launch_one<TILE_256x256_PP, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_256x128_W8: return launch_one<TILE_256x128_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_128x128_W8: return launch_one<TILE_128x128_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
   }
 }

@@ -9,7 +9,7 @@ from oracle import hot_path as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = list(range(12))  # every instantiated tile shape (TileId)
+TILES = list(range(14))  # every instantiated tile shape (TileId)
 
 
 def run_gemm(pkg, dev, a, b, layout, **kw):
@@ -51,7 +51,7 @@ def test_gemm_bias_exact_every_tile(pkg, dev, force_tile, tile):
 @pytest.mark.parametrize("layout", ["nn", "nt"])
 @pytest.mark.parametrize("M,N,K", [(1, 8, 8), (33, 72, 40), (130, 264, 200), (300, 136, 520), (197, 64, 64),
                                    (64, 64, 0), (5, 24, 8)])
-@pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10, 11])
+@pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10, 11, 12, 13])
 def test_gemm_ragged_shapes(pkg, dev, force_tile, layout, M, N, K, tile):
     force_tile(tile)
     a = uniform((M, K), 2)
@@ -72,7 +72,7 @@ def test_gemm_unaligned_elementwise_path(pkg, dev, layout, M, N, K, lda):
 
 
 @pytest.mark.parametrize("epi", ["bias", "gelu_tanh", "bias_gelu_tanh"])
-@pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10, 11])
+@pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10, 11, 12, 13])
 def test_gemm_epilogues(pkg, dev, force_tile, epi, tile):
     force_tile(tile)
     M, N, K = 300, 264, 256
@@ -84,7 +84,7 @@ def test_gemm_epilogues(pkg, dev, force_tile, epi, tile):
     assert ref.max_rel_err(np32(c), exp) <= TOL
 
 
-@pytest.mark.parametrize("tile", [None, 0, 1, 2, 3, 4, 11])
+@pytest.mark.parametrize("tile", [None, 0, 1, 2, 3, 4, 11, 12, 13])
 def test_gemm_silu_mul(pkg, dev, force_tile, tile):
     force_tile(tile)
     M, I, K = 200, 320, 256
