@@ -163,7 +163,7 @@ int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int
 }
 
 int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                  int64_t ldx, int64_t ldw, int64_t ldy, void* stream) {
+                  int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream) {
   const char* name = "hxmi_gemv_f16";
   REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", name);
   if (M == 0 || N == 0) return ok();
@@ -187,7 +187,22 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
   p.ldw = ldw;
   p.ldy = ldy;
   p.w_int8 = 0;
+  p.ws = workspace_bytes > 0 ? workspace : nullptr;
+  p.ws_bytes = workspace_bytes > 0 ? workspace_bytes : 0;
   return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
+}
+
+int64_t hxmi_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || M > 16 || N <= 0 || K <= 0 || K % 8 || N % 4) return 0;
+  hxmi::GemvProblem g{};
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.ldx = K;
+  g.ldw = K;
+  g.ldy = N;
+  g.w_int8 = 0;
+  return hxmi::gemv_workspace_bytes(g);
 }
 
 int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const void* bias, void* y, int64_t M,
@@ -216,6 +231,8 @@ int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const vo
   p.ldw = ldw;
   p.ldy = ldy;
   p.w_int8 = 1;
+  p.ws = workspace_bytes > 0 ? workspace : nullptr;
+  p.ws_bytes = workspace_bytes > 0 ? workspace_bytes : 0;
   if (M <= 16) return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
   REQUIRE(N % 8 == 0, "%s: M > 16 needs N %% 8 == 0", name);
   return from_hip(hxmi::launch_w8a16_gemm(p, workspace_bytes > 0 ? workspace : nullptr,
@@ -224,7 +241,7 @@ int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const vo
 }
 
 int64_t hxmi_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 16 || N <= 0 || K <= 0) return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
   hxmi::GemvProblem g{};
   g.M = M;
   g.N = N;
@@ -234,6 +251,7 @@ int64_t hxmi_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   g.ldy = N;
   g.x = g.W = g.y = (void*)(uintptr_t)256;
   g.w_int8 = 1;
+  if (M <= 16) return K % 16 || N % 4 ? 0 : hxmi::gemv_workspace_bytes(g);
   return hxmi::gemm_workspace_bytes(hxmi::w8a16_as_gemm(g));
 }
 

@@ -19,6 +19,8 @@
 // lines), which lets the weights stream with the non-temporal policy.
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "hxmi_common.h"
 #include "hxmi_internal.h"
 
@@ -33,7 +35,15 @@ struct VArgs {
   char* y;
   int M, N, K;
   int64_t ldx, ldw, ldy;
+  // K split over kg workgroups per row group (kg > 1): workspace with one
+  // arrival counter per 16-row tile, then kg fp32 partial tiles per tile;
+  // epoch tags the call so counters left by other calls count as zero
+  int kg;
+  char* ws;
+  unsigned long long epoch;
 };
+
+__host__ __device__ constexpr int64_t gemv_counter_bytes(int64_t tiles) { return (tiles * 8 + 255) / 256 * 256; }
 
 __device__ __forceinline__ float4v mfma16(short8v a, short8v b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a), __builtin_bit_cast(half8v, b),
@@ -61,11 +71,15 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * (TPB * 16);
+  const int rg = blockIdx.x / a.kg, kgi = blockIdx.x % a.kg;  // row group, K group
+  const int n0 = rg * (TPB * 16);
   const int nsteps = (a.K + KSTEP - 1) / KSTEP;
-  const int per_wave = (nsteps + KS - 1) / KS;
-  const int s_begin = w * per_wave;
-  const int s_end = min(nsteps, s_begin + per_wave);
+  const int per_group = (nsteps + a.kg - 1) / a.kg;
+  const int g_begin = min(nsteps, kgi * per_group);
+  const int g_end = min(nsteps, g_begin + per_group);
+  const int per_wave = (g_end - g_begin + KS - 1) / KS;
+  const int s_begin = g_begin + w * per_wave;
+  const int s_end = min(g_end, s_begin + per_wave);
 
   const int r16 = lane & 15, kq = lane >> 4;  // row within tile, k quarter
   const int esz = I8 ? 1 : 2;
@@ -135,6 +149,42 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
       sum = red[0][t][lane];
 #pragma unroll
       for (int q = 1; q < KS; ++q) sum += red[q][t][lane];
+    }
+    if (a.kg > 1) {
+      // Split K: store this K group's partial tile (system-coherent stores,
+      // visible to every XCD once vmcnt drains), arrive on the tile's
+      // counter; the last K group adds all partials in K-group order and
+      // finishes the tile.
+      constexpr int kCoherent = 17;  // sc0 | sc1
+      const int tile = rg * TPB + t;
+      const int tiles = (a.N + TPB * 16 - 1) / (TPB * 16) * TPB;
+      unsigned long long* cnt = (unsigned long long*)a.ws + tile;
+      float* part = (float*)(a.ws + gemv_counter_bytes(tiles)) + (int64_t)tile * a.kg * 256;
+      const __amdgpu_buffer_rsrc_t rP = make_rsrc(part, a.kg * 1024);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, sum), rP, (uint32_t)(kgi * 1024 + lane * 16), 0,
+                                             kCoherent);
+      wait_vmcnt0();
+      unsigned long long arrived = 0;
+      if (lane == 0) {
+        // first guess: the state the last call with this epoch left (a graph
+        // replay); a failed exchange returns the current value, so a wrong
+        // guess costs one round trip and every later failure means another
+        // K group arrived (lock-free)
+        unsigned long long cur = a.epoch << 8;
+        for (int tries = 0; tries < (1 << 16); ++tries) {
+          arrived = (cur >> 8) == a.epoch ? (cur & 255u) : 0ull;
+          if (__hip_atomic_compare_exchange_strong(cnt, &cur, (a.epoch << 8) | (arrived + 1), __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            break;
+        }
+      }
+      arrived = __shfl(arrived, 0, 64);
+      if (arrived + 1 != (unsigned long long)a.kg) continue;
+      sum = float4v{0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < a.kg; ++g)
+        sum += __builtin_bit_cast(float4v,
+                                  __builtin_amdgcn_raw_buffer_load_b128(rP, (uint32_t)(g * 1024 + lane * 16), 0, kCoherent));
+      if (lane == 0) __hip_atomic_store(cnt, a.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // D[n][m]: lane holds m = lane % 16, n = 4*(lane / 16) + 0..3
     const int m = lane & 15;
@@ -269,9 +319,27 @@ hipError_t launch_valu_sel(const VArgs& v, hipStream_t stream) {
 
 template <int TPB, int KS, bool I8>
 hipError_t launch_cfg(const VArgs& v, hipStream_t stream) {
-  constexpr int UNR = TPB >= 4 ? 2 : 4;
-  const int blocks = (v.N + TPB * 16 - 1) / (TPB * 16);
-  hipLaunchKernelGGL((gemv_mfma<TPB, KS, I8, UNR>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+  // loads in flight per wave: a wave whose K range is long (few tiles, large
+  // K) issues 16 steps at a time; short ranges keep 4 (2 for 4-tile groups)
+  const int kstep = I8 ? 64 : 32;
+  const int per_wave = ((v.K + kstep - 1) / kstep + KS * v.kg - 1) / (KS * v.kg);
+  const int blocks = (v.N + TPB * 16 - 1) / (TPB * 16) * v.kg;
+  int unr = TPB >= 4 ? 2 : (per_wave >= 12 ? (TPB == 1 ? 16 : 8) : 4);
+  if (const char* e = getenv("HXMI_GEMV_UNR")) unr = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : (TPB >= 4 ? 2 : 4));
+  if constexpr (TPB < 4) {
+    if (unr == 16 && TPB == 1) {
+      hipLaunchKernelGGL((gemv_mfma<1, KS, I8, 16>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+      return hipGetLastError();
+    }
+    // (16 waves per workgroup leave 128 VGPRs: 8 steps of two tiles would spill)
+    if constexpr (TPB == 1 || KS <= 8) {
+      if (unr == 8) {
+        hipLaunchKernelGGL((gemv_mfma<TPB, KS, I8, 8>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+        return hipGetLastError();
+      }
+    }
+  }
+  hipLaunchKernelGGL((gemv_mfma<TPB, KS, I8, (TPB >= 4 ? 2 : 4)>), dim3(blocks), dim3(KS * 64), 0, stream, v);
   return hipGetLastError();
 }
 
@@ -294,6 +362,65 @@ hipError_t launch_sel(int tpb, int ks, const VArgs& v, hipStream_t stream) {
 
 }  // namespace
 
+// Launch plan of a decode GEMV: rows per workgroup (TPB tiles of 16), waves
+// splitting K inside a workgroup (KS), the row-streaming kernel (valu), and
+// K groups across workgroups (kg).
+struct GemvPlan {
+  int tpb = 1, ks = 8, kg = 1;
+  bool valu = false;
+};
+
+static GemvPlan gemv_plan(const GemvProblem& p) {
+  GemvPlan g;
+  // TPB and KS from a sweep of every (TPB, KS) on the Qwen2.5-0.5B decode
+  // shapes: one 16-row tile per workgroup keeps the most workgroups in flight
+  // for M <= 4; for M > 4 the x fragments are shared by more rows (TPB 2-4)
+  // once there are enough tiles; 8 waves per workgroup unless a wave would
+  // get < 2 K-steps.
+  const int64_t tiles16 = (p.N + 15) / 16;
+  if (p.M > 4) g.tpb = tiles16 >= 600 ? 4 : (tiles16 >= 300 ? 2 : 1);
+  if (p.w_int8 && p.M <= 4 && tiles16 >= 4096) g.tpb = 2;
+  const int kstep = p.w_int8 ? 64 : 32;
+  const int64_t nsteps = (p.K + kstep - 1) / kstep;
+  while (g.ks > 4 && nsteps / g.ks < 2) g.ks /= 2;
+  // tuning overrides (launch shape only; every shape computes the same sums)
+  if (const char* e = getenv("HXMI_GEMV_TPB")) g.tpb = atoi(e) == 4 ? 4 : (atoi(e) == 2 ? 2 : 1);
+  if (const char* e = getenv("HXMI_GEMV_KS")) g.ks = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : 4);
+  // vector-ALU row streaming: small M, x fits the LDS, enough row groups
+  // (measured on the Qwen2.5-0.5B shapes: the row-streaming kernel wins for
+  // long weight matrices -- lm_head -- up to M = 8 (int8: 4) and for M = 1
+  // from N = 4096; the MFMA tiles win where K must be split across waves)
+  const int kstep_v = p.w_int8 ? 128 : 64;
+  const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
+  const bool fits = p.M <= 8 && p.M * kpad * 2 <= 64 * 1024;
+  g.valu = fits && (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
+  if (const char* e = getenv("HXMI_GEMV_PATH")) g.valu = (e[0] == 'v') && fits;
+  if (g.valu) return g;
+  // few row groups, each streaming a long K (e.g. a down projection
+  // 4864 -> 896): split K over 2-4 workgroups per row group.  Combining the
+  // partial tiles costs ~2 us of round trips to memory, so (measured on the
+  // Qwen2.5-0.5B and TinyLlama down projections, M 1-16) it pays from
+  // ~144 KiB of weights per workgroup (M > 8 does twice the MFMA work per
+  // byte: 72 KiB)
+  const int64_t groups = (p.N + g.tpb * 16 - 1) / (g.tpb * 16);
+  const int64_t wg_bytes = (int64_t)g.tpb * 16 * p.K * (p.w_int8 ? 1 : 2) * (p.M > 8 ? 2 : 1);
+  if (groups < 192 && wg_bytes >= (144 << 10)) {
+    int kg = (int)((192 + groups / 2) / groups);
+    kg = kg < 2 ? 2 : (kg > 4 ? 4 : kg);
+    while (kg > 1 && nsteps / kg < 2 * g.ks) --kg;
+    g.kg = kg;
+  }
+  if (const char* e = getenv("HXMI_GEMV_KG")) g.kg = atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
+  return g;
+}
+
+int64_t gemv_workspace_bytes(const GemvProblem& p) {
+  const GemvPlan g = gemv_plan(p);
+  if (g.valu || g.kg <= 1) return 0;
+  const int64_t tiles = (p.N + g.tpb * 16 - 1) / (g.tpb * 16) * g.tpb;  // 16-row tiles of whole row groups
+  return gemv_counter_bytes(tiles) + tiles * g.kg * 1024;
+}
+
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0) return hipSuccess;
   VArgs v;
@@ -308,33 +435,18 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.ldx = p.ldx;
   v.ldw = p.ldw;
   v.ldy = p.ldy;
-  // Rows per workgroup (TPB tiles of 16) and waves splitting K (KS), from a
-  // sweep of every (TPB, KS) on the Qwen2.5-0.5B decode shapes: one 16-row
-  // tile per workgroup keeps the most workgroups in flight for M <= 4; for
-  // M > 4 the x fragments are shared by more rows (TPB 2-4) once there are
-  // enough tiles; 8 waves per workgroup unless a wave would get < 2 K-steps.
-  const int64_t tiles16 = (p.N + 15) / 16;
-  int tpb = 1;
-  if (p.M > 4) tpb = tiles16 >= 600 ? 4 : (tiles16 >= 300 ? 2 : 1);
-  if (p.w_int8 && p.M <= 4 && tiles16 >= 4096) tpb = 2;
-  const int kstep = p.w_int8 ? 64 : 32;
-  const int64_t nsteps = (p.K + kstep - 1) / kstep;
-  int ks = 8;
-  while (ks > 4 && nsteps / ks < 2) ks /= 2;
-  // tuning overrides (launch shape only; every shape computes the same sums)
-  if (const char* e = getenv("HXMI_GEMV_TPB")) tpb = atoi(e) == 4 ? 4 : (atoi(e) == 2 ? 2 : 1);
-  if (const char* e = getenv("HXMI_GEMV_KS")) ks = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : 4);
-  // vector-ALU row streaming: small M, x fits the LDS, enough row groups
-  const int kstep_v = p.w_int8 ? 128 : 64;
-  const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
-  // (measured on the Qwen2.5-0.5B shapes: the row-streaming kernel wins for
-  // long weight matrices -- lm_head -- up to M = 8 (int8: 4) and for M = 1
-  // from N = 4096; the MFMA tiles win where K must be split across waves)
-  const bool fits = p.M <= 8 && p.M * kpad * 2 <= 64 * 1024;
-  bool valu = fits && (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
-  if (const char* e = getenv("HXMI_GEMV_PATH")) valu = (e[0] == 'v') && fits;
-  if (valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
-  return p.w_int8 ? launch_sel<true>(tpb, ks, v, stream) : launch_sel<false>(tpb, ks, v, stream);
+  v.kg = 1;
+  v.ws = nullptr;
+  v.epoch = 0;
+  const GemvPlan g = gemv_plan(p);
+  if (g.valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
+  if (g.kg > 1 && p.ws && p.ws_bytes >= gemv_workspace_bytes(p) && ((uintptr_t)p.ws % 256) == 0) {
+    static std::atomic<unsigned long long> calls{1};
+    v.kg = g.kg;
+    v.ws = (char*)p.ws;
+    v.epoch = calls.fetch_add(1) & ((1ull << 56) - 1);
+  }
+  return p.w_int8 ? launch_sel<true>(g.tpb, g.ks, v, stream) : launch_sel<false>(g.tpb, g.ks, v, stream);
 }
 
 }  // namespace hxmi

@@ -88,9 +88,13 @@ struct GemvProblem {
   int64_t M, N, K;
   int64_t ldx, ldw, ldy;
   int w_int8;
+  void* ws;  // optional workspace for K split over workgroups
+  int64_t ws_bytes;
 };
 
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream);
+// Workspace bytes launch_gemv can use for p (0: it never splits K).
+int64_t gemv_workspace_bytes(const GemvProblem& p);
 
 // W8A16 GEMM for larger M (MFMA, int8 weights dequantised in registers).
 hipError_t launch_w8a16_gemm(const GemvProblem& p, void* ws, int64_t ws_bytes, hipStream_t stream);

@@ -37,7 +37,8 @@ SIGNATURES = {
     "hxmi_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
     "hxmi_bgemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_bgemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
-    "hxmi_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
+    "hxmi_gemv_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "hxmi_gemv_w8a16": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "hxmi_w8a16_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "hxmi_rmsnorm_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
@@ -311,8 +312,10 @@ def gemv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
     if out is None:
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
     ldy = _rowmajor(out, "out")
-    _check(load_library().hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, ldx, ldw,
-                                        ldy, _stream(x)))
+    lib = load_library()
+    ws = _workspace(lib.hxmi_gemv_workspace_bytes(M, N, K), x.device)
+    _check(lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, ldx, ldw, ldy,
+                             _ptr(ws), 0 if ws is None else ws.numel() * 4, _stream(x)))
     return out
 
 

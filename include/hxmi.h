@@ -104,11 +104,19 @@ int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int
  * Decode GEMV/skinny GEMM: y[M,N] = x[M,K] . W[N,K]^T (+ bias[N]), fp16,
  * fp32 accumulation, any M (M <= 16 streams W once through the GEMV kernel,
  * larger M goes to the GEMM).  bias may be NULL.
+ * workspace / workspace_bytes: optional caller-owned device scratch
+ * (256-byte aligned).  With few output rows and a long K (a down
+ * projection) the GEMV splits K over workgroups, which combine their fp32
+ * partial tiles there; it needs hxmi_gemv_workspace_bytes() bytes.  NULL / 0
+ * runs unsplit.  Two calls must not share a workspace concurrently.
  * Replaces: the M = 1 matmul_transpose_b that the reference sends through
  * the same generic HVX schedule (TilingPass.cpp:108-251); it has no GEMV.
  */
 int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                  int64_t ldx, int64_t ldw, int64_t ldy, void* stream);
+                  int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes a contiguous hxmi_gemv_f16 call of this shape can use (0: never split). */
+int64_t hxmi_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*
  * Weight-only int8 linear: y[m,n] = scale[n] * sum_k x[m,k] * Wq[n,k] (+ bias[n]).
@@ -116,8 +124,8 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
  * scale).  Weights are converted to fp16 exactly in registers; the scale
  * multiplies the fp32 sum.  Requires K % 16 == 0, ldw % 16 == 0, N % 4 == 0.
  * M <= 16 streams Wq once (GEMV kernel); larger M runs the MFMA GEMM with
- * the int8 operand, which may split K into the optional workspace (see
- * hxmi_gemm_f16; size from hxmi_w8a16_workspace_bytes).
+ * the int8 operand.  Either may split K into the optional workspace (see
+ * hxmi_gemv_f16 / hxmi_gemm_f16; size from hxmi_w8a16_workspace_bytes).
  * Replaces: no reference kernel (only quant.qcast/dcast lowering to arith,
  * LinalgToLLVMPass.cpp:203-209); defined by the weight-only int8 configs.
  */
@@ -125,7 +133,8 @@ int hxmi_gemv_w8a16(const void* x, const int8_t* Wq, const void* scale, const vo
                     int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes a contiguous hxmi_gemv_w8a16 call of this shape can use. */
+/* Workspace bytes a contiguous hxmi_gemv_w8a16 call of this shape can use
+ * (M <= 16: the GEMV's K split, as hxmi_gemv_f16; larger M: the GEMM's). */
 int64_t hxmi_w8a16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*

@@ -68,7 +68,7 @@ def test_empty_problems_are_noops(pkg):
     lib = pkg.load_library()
     assert lib.hxmi_gemm_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, 1, 0, 1.0, None, 0, None) == 0
     assert lib.hxmi_last_error() == b""
-    assert lib.hxmi_gemv_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, None) == 0
+    assert lib.hxmi_gemv_f16(None, None, None, None, 0, 8, 8, 8, 8, 8, None, 0, None) == 0
     assert lib.hxmi_rmsnorm_f16(None, None, None, 0, 16, 16, 16, 1e-5, None) == 0
     assert lib.hxmi_softmax_f16(None, None, 4, 0, 0, 0, 1.0, None) == 0
 
@@ -115,5 +115,11 @@ def test_workspace_queries(pkg):
     # 4096^3 fills the GPU without splitting; batched / short-K never split
     assert lib.hxmi_gemm_workspace_bytes(4096, 4096, 4096, 1, 0) == 0
     assert lib.hxmi_gemm_workspace_bytes(512, 2048, 512, 1, 0) == 0
-    assert lib.hxmi_w8a16_workspace_bytes(16, 896, 4864) == 0  # GEMV path
+    # decode GEMV: a down projection (few rows, long K) splits K over
+    # workgroups; wide outputs and the lm_head never do
+    assert lib.hxmi_w8a16_workspace_bytes(16, 896, 4864) > 0
+    assert lib.hxmi_gemv_workspace_bytes(1, 896, 4864) > 0
+    assert lib.hxmi_gemv_workspace_bytes(1, 4864, 896) == 0
+    assert lib.hxmi_gemv_workspace_bytes(1, 151936, 896) == 0
+    assert lib.hxmi_gemv_workspace_bytes(17, 896, 4864) == 0  # the GEMM's case
     assert lib.hxmi_w8a16_workspace_bytes(256, 896, 4864) > 0

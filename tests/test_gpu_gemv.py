@@ -150,3 +150,112 @@ def test_w8a16_bias_and_scale_linearity(pkg, dev):
     torch.cuda.synchronize()
     assert ref.max_rel_err(np32(y1.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
     assert ref.max_rel_err(np32(y2.cpu()), 2 * ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy())) <= TOL
+
+
+@pytest.fixture
+def gemv_kgroups(monkeypatch):
+    """Force the number of workgroups that split K per row group (1 = unsplit)."""
+
+    def force(kg):
+        monkeypatch.setenv("HXMI_GEMV_PATH", "mfma")
+        monkeypatch.setenv("HXMI_GEMV_KG", str(kg))
+
+    return force
+
+
+@pytest.mark.parametrize("kg", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("N,K", [(896, 4864), (72, 4104), (8, 8200)])
+def test_gemv_k_groups(pkg, dev, gemv_kgroups, kg, M, N, K):
+    # K split over workgroups that combine fp32 partial tiles in the workspace;
+    # ragged K groups (K not a multiple of kg steps) and a partial 16-row tile
+    gemv_kgroups(kg)
+    x = normal((M, K), 31 + M)
+    w = normal((N, K), 32, 0.05)
+    b = normal((N,), 33)
+    y = pkg.gemv(x.to(dev), w.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("kg", [2, 5, 8])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_w8a16_k_groups(pkg, dev, gemv_kgroups, kg, M):
+    gemv_kgroups(kg)
+    N, K = 904, 4864
+    x = normal((M, K), 41 + M)
+    q, s = int8_weights(N, K, 42)
+    b = normal((N,), 43)
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
+
+
+def test_w8a16_onehot_exact_k_groups(pkg, dev, gemv_kgroups):
+    # one-hot rows land in one K group; the others add exact zeros
+    gemv_kgroups(4)
+    d = np.load(GOLDEN / "w8_onehot.npz")
+    q, cols = torch.from_numpy(d["q"]), d["cols"]
+    M = 5
+    rows = np.resize(np.arange(len(cols)), M)
+    x = torch.zeros((M, q.shape[1]), dtype=torch.float16)
+    x[np.arange(M), cols[rows]] = 1
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), torch.ones(q.shape[0], dtype=torch.float16, device=dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().astype(np.int32), d["y"][rows])
+
+
+def test_gemv_down_projection_splits_by_default(pkg, dev):
+    """The Qwen2.5-0.5B down projection (4864 -> 896) splits K by default; the
+    result is deterministic (partials are added in K-group order) and one
+    workspace serves calls of different shapes back to back."""
+    lib = pkg.load_library()
+    assert lib.hxmi_gemv_workspace_bytes(1, 896, 4864) > 0
+    assert lib.hxmi_gemv_workspace_bytes(1, 4864, 896) == 0
+    nbytes = max(lib.hxmi_gemv_workspace_bytes(m, 896, 4864) for m in (1, 16))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    w = normal((896, 4864), 51, 0.05).to(dev)
+    outs = []
+    for M in (1, 16, 1, 16, 1):
+        x = normal((M, 4864), 52 + M).to(dev)
+        y = torch.empty((M, 896), dtype=torch.float16, device=dev)
+        rc = lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, 896, 4864, 4864, 4864, 896,
+                               ws.data_ptr(), nbytes, None)
+        assert rc == 0, lib.hxmi_last_error()
+        outs.append(y.cpu())
+        assert ref.max_rel_err(np32(outs[-1]), ref.linear(x.cpu().numpy(), w.cpu().numpy())) <= TOL
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[0], outs[4]) and torch.equal(outs[1], outs[3])
+
+
+def test_gemv_k_groups_graph_replays(pkg, dev):
+    """Captured split-K GEMV: the arrival counters reset themselves, so every
+    replay (with eager calls on the same workspace between them) matches."""
+    M, N, K = 1, 896, 4864
+    lib = pkg.load_library()
+    nbytes = lib.hxmi_gemv_workspace_bytes(M, N, K)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    x = normal((M, K), 61).to(dev)
+    w = normal((N, K), 62, 0.05).to(dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    s = torch.cuda.Stream()
+
+    def call(stream):
+        rc = lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, N, K, K, K, N, ws.data_ptr(),
+                               nbytes, stream)
+        assert rc == 0, lib.hxmi_last_error()
+
+    call(None)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(s.cuda_stream)
+    for _ in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        call(None)  # eager call between replays, same workspace
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
