@@ -3,6 +3,8 @@
 // multiple of 8, misaligned pointers).
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "gemm_impl.h"
 
 namespace hxmi {
@@ -141,54 +143,6 @@ int gemm_pick_tile(const GemmProblem& p) {
 namespace gemm {
 namespace {
 
-struct ReduceArgs {
-  const float* W;  // [splits][M][N] fp32 partial sums
-  char* C;
-  const char* bias;
-  int64_t M, N, Nout, ldc, splits;
-  float alpha;
-  int epi;
-};
-
-// Split-K reduction + epilogue: every thread produces 4 consecutive output
-// columns from the fp32 partial sums (for SiLU-mul, 4 gate and the 4 up
-// columns 16 further along in the packed layout).
-template <typename T>
-__global__ __launch_bounds__(256) void splitk_reduce(ReduceArgs r) {
-  const int64_t groups = r.Nout / 4;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= r.M * groups) return;
-  const int64_t m = idx / groups;
-  const int64_t o = (idx - m * groups) * 4;
-  const int64_t plane = r.M * r.N;
-  float v[4];
-  if (r.epi == EPI_SILU_MUL) {
-    const int64_t pc = 32 * (o / 16) + (o % 16);
-    float4v g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t s = 0; s < r.splits; ++s) {
-      g += *(const float4v*)(r.W + s * plane + m * r.N + pc);
-      u += *(const float4v*)(r.W + s * plane + m * r.N + pc + 16);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = silu(g[q] * r.alpha) * (u[q] * r.alpha);
-  } else {
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t s = 0; s < r.splits; ++s) acc += *(const float4v*)(r.W + s * plane + m * r.N + o);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = acc[q] * r.alpha;
-    if (r.epi == EPI_BIAS || r.epi == EPI_BIAS_GELU_TANH) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] += (float)((const T*)r.bias)[o + q];
-    }
-    if (r.epi == EPI_GELU_TANH || r.epi == EPI_BIAS_GELU_TANH) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = gelu_tanh(v[q]);
-    }
-  }
-  T t[4] = {(T)v[0], (T)v[1], (T)v[2], (T)v[3]};
-  *(short4v*)(r.C + (m * r.ldc + o) * (int64_t)sizeof(T)) = __builtin_bit_cast(short4v, t);
-}
-
 int tile_for(const GemmProblem& p) {
   int tile = p.tile >= 0 ? p.tile : env_int("HXMI_GEMM_TILE", -1);
   if (tile < 0 || tile >= TILE_COUNT) tile = gemm_pick_tile(p);
@@ -236,22 +190,49 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 }  // namespace gemm
 
 // Split K into slices when the output has too few tiles to occupy the 256
-// CUs and K is long enough that each slice still runs many K-steps.
+// CUs and K is long enough that each slice still runs many K-steps.  Split
+// problems run 64x128 tiles (4 waves, up to three per CU); the slice count
+// aims at ~480 of them, each slice keeping >= 1024 of K.  Measured on the
+// TinyLlama down projection (512x2048x5632: 431 -> 464 TFLOP/s against
+// 128x128 tiles) and ViT-B/16 fc2 (1576x768x3072: 316 -> 376); with K below
+// 3072 (the 512-token QKV and O projections) every split measured slower.
 int gemm_splits(const GemmProblem& p) {
   if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || !gemm_fast_path_ok(p)) return 1;
   if (const char* e = getenv("HXMI_SPLITK")) return atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
-  // 128x128 output tiles are the unit of work split-K is judged by; below
-  // K = 3072 the extra reduction pass costs more than the idle CUs
-  const int64_t tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (tiles >= 128 || p.K < 3072) return 1;
-  int s = 1;
-  while (s < 8 && tiles * s < 256 && p.K / (2 * s) >= 1024) s *= 2;
+  const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 127) / 128);
+  if (tiles >= 384 || p.K < 3072) return 1;
+  int s = (int)((480 + tiles / 2) / tiles);
+  s = s < 1 ? 1 : (s > 4 ? 4 : s);
+  while (s > 1 && p.K / s < 1024) --s;
   return s;
 }
 
+// The split-K launch of p: K slices of kc (a multiple of the 64-deep K-step)
+// as a batch of GEMMs into the same output (sC = 0), the tile they run and
+// the fix-up workspace they need.  False when p does not split.
+static bool split_plan(const GemmProblem& p, GemmProblem& q, int& tile, int64_t& need) {
+  const int splits = gemm_splits(p);
+  if (splits <= 1) return false;
+  q = p;
+  const int64_t kc = ((p.K + splits - 1) / splits + 63) / 64 * 64;
+  q.K = kc;
+  q.batch = (p.K + kc - 1) / kc;
+  q.sA = kc;
+  q.sB = p.b_nt ? kc : kc * p.ldb;
+  q.sC = 0;
+  if (q.tile < 0 && gemm::env_int("HXMI_GEMM_TILE", -1) < 0) q.tile = TILE_64x128;
+  tile = gemm::tile_for(q);
+  const gemm::TileShape s = gemm::kTiles[tile];
+  const int64_t tiles = ((p.M + s.BM - 1) / s.BM) * ((p.N + s.BN - 1) / s.BN);
+  need = gemm::fix_counter_bytes(tiles) + tiles * q.batch * s.BM * s.BN * 4;
+  return q.batch > 1;
+}
+
 int64_t gemm_workspace_bytes(const GemmProblem& p) {
-  const int s = gemm_splits(p);
-  return s > 1 ? (int64_t)s * p.M * p.N * 4 : 0;
+  GemmProblem q;
+  int tile;
+  int64_t need;
+  return split_plan(p, q, tile, need) ? need : 0;
 }
 
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream) {
@@ -291,48 +272,18 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream) {
     return hipGetLastError();
   }
 
-  const int splits = gemm_splits(p);
-  const int64_t need = splits > 1 ? (int64_t)splits * p.M * p.N * 4 : 0;
-  if (splits > 1 && p.ws && p.ws_bytes >= need && ((uintptr_t)p.ws % 16) == 0) {
-    // slices of kc (a multiple of the 64-deep K-step) as a batch of GEMMs
-    // writing fp32 partial sums, then one reduction with the epilogue
-    GemmProblem q = p;
-    const int64_t kc = ((p.K + splits - 1) / splits + 63) / 64 * 64;
-    const int64_t used = (p.K + kc - 1) / kc;
-    q.K = kc;
-    q.batch = used;
-    q.sA = kc;
-    q.sB = p.b_nt ? kc : kc * p.ldb;
-    q.C = p.ws;
-    q.ldc = p.N;
-    q.sC = p.M * p.N;
-    q.out_f32 = 1;
-    q.epilogue = EPI_NONE;
-    q.alpha = 1.f;
-    q.bias = nullptr;
-    q.tile = p.tile;
-    const int tile = gemm::tile_for(q);
-    gemm::KArgs k = gemm::make_kargs(q, tile);
-    k.k_last = (int)(p.K - (used - 1) * kc);
-    hipError_t e = gemm::launch_fast(q, tile, k, stream);
-    if (e != hipSuccess) return e;
-    gemm::ReduceArgs r;
-    r.W = (const float*)p.ws;
-    r.C = (char*)p.C;
-    r.bias = (const char*)p.bias;
-    r.M = p.M;
-    r.N = p.N;
-    r.Nout = p.epilogue == EPI_SILU_MUL ? p.N / 2 : p.N;
-    r.ldc = p.ldc;
-    r.splits = used;
-    r.alpha = p.alpha;
-    r.epi = p.epilogue;
-    const int64_t blocks = (p.M * (r.Nout / 4) + 255) / 256;
-    if (p.dtype == DT_BF16)
-      hipLaunchKernelGGL(gemm::splitk_reduce<__bf16>, dim3((unsigned)blocks), dim3(256), 0, stream, r);
-    else
-      hipLaunchKernelGGL(gemm::splitk_reduce<_Float16>, dim3((unsigned)blocks), dim3(256), 0, stream, r);
-    return hipGetLastError();
+  GemmProblem q;
+  int qtile;
+  int64_t need;
+  if (split_plan(p, q, qtile, need) && p.ws && p.ws_bytes >= need && ((uintptr_t)p.ws % 256) == 0) {
+    // K slices as a batch into one output; the last slice to finish a tile
+    // adds the fp32 partials (in the workspace) and runs the epilogue
+    static std::atomic<unsigned long long> calls{1};
+    gemm::KArgs k = gemm::make_kargs(q, qtile);
+    k.k_last = (int)(p.K - (q.batch - 1) * q.K);
+    k.fix = (char*)p.ws;
+    k.epoch = calls.fetch_add(1) & ((1ull << 56) - 1);
+    return gemm::launch_fast(q, qtile, k, stream);
   }
 
   const int tile = gemm::tile_for(p);

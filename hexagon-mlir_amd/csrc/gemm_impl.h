@@ -43,7 +43,16 @@ struct KArgs {
   int group_m;
   int k_last;  // > 0: the last batch entry has this K (split-K: a ragged last slice)
   float rms_eps;  // RMS kernels: epsilon of the row RMSNorm folded into the GEMM
+  // Split-K with in-kernel fix-up (fix != nullptr): the batch entries are K
+  // slices of one output (sC = 0).  fix holds one arrival counter per output
+  // tile, then batch fp32 partial tiles per output tile in fragment order;
+  // epoch tags the call so counters left by other calls read as zero.
+  char* fix;
+  unsigned long long epoch;
 };
+
+// Bytes of the arrival counters at the head of a split-K fix-up workspace.
+__host__ __device__ constexpr int64_t fix_counter_bytes(int64_t tiles) { return (tiles * 8 + 255) / 256 * 256; }
 
 template <typename T>
 struct Mfma;
@@ -510,6 +519,65 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       const float r = rsqrtf(tot / (float)a.K + a.rms_eps);
 #pragma unroll
       for (int i = 0; i < TN; ++i) acc[i][j] *= r;
+    }
+  }
+
+  if constexpr (!OUTF32) {
+    if (a.fix) {
+      // Split-K fix-up: store this K slice's accumulators (system-coherent,
+      // visible to every XCD once vmcnt drains), arrive on the output
+      // tile's counter; the last slice to arrive adds all partial tiles in
+      // slice order (deterministic) and runs the epilogue.
+      constexpr int kCoherent = 17;  // sc0 | sc1
+      constexpr int TILE_B = BM * BN * 4;
+      const int tiles = a.tiles_m * a.tiles_n;
+      const int tile = tm * a.tiles_n + tn;
+      unsigned long long* cnt = (unsigned long long*)a.fix + tile;
+      const __amdgpu_buffer_rsrc_t rP =
+          make_rsrc(a.fix + fix_counter_bytes(tiles) + (int64_t)tile * a.batch * TILE_B, (uint32_t)(a.batch * TILE_B));
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const float4v v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+            const uint32_t off = (uint32_t)(b * TILE_B + (((i * TM + j) * 4 + g) * NT + threadIdx.x) * 16);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, v), rP, off, 0, kCoherent);
+          }
+      wait_vmcnt0();
+      __shared__ int is_last;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        // first guess: the state the last call with this epoch left (a graph
+        // replay); a failed exchange returns the current value, and every
+        // later failure means another slice arrived (lock-free)
+        unsigned long long cur = a.epoch << 8, arrived = 0;
+        for (int tries = 0; tries < (1 << 16); ++tries) {
+          arrived = (cur >> 8) == a.epoch ? (cur & 255u) : 0ull;
+          if (__hip_atomic_compare_exchange_strong(cnt, &cur, (a.epoch << 8) | (arrived + 1), __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            break;
+        }
+        is_last = arrived + 1 == (unsigned long long)a.batch;
+        if (is_last) __hip_atomic_store(cnt, a.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!is_last) return;
+      for (int sl = 0; sl < a.batch; ++sl) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const uint32_t off = (uint32_t)(sl * TILE_B + (((i * TM + j) * 4 + g) * NT + threadIdx.x) * 16);
+              const float4v v =
+                  __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rP, off, 0, kCoherent));
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[i][j][4 * g + q] = sl == 0 ? v[q] : acc[i][j][4 * g + q] + v[q];
+            }
+      }
     }
   }
 

@@ -16,7 +16,10 @@
 // The MFMA operand layout makes each wave instruction read 64 bytes of 16
 // rows, half cache lines.  For M <= 8 a second kernel (gemv_valu) uses the
 // vector ALUs instead: a lane load then covers 8 rows x 128 bytes (whole
-// lines), which lets the weights stream with the non-temporal policy.
+// lines), which lets the weights stream with the non-temporal policy.  For
+// M > 8 its x reads from LDS grow with M and bound it, so long weight
+// matrices with K <= 1024 (the lm_head) use a third kernel (gemv_xreg) that
+// holds x in registers and gives each wave whole 16-row tiles.
 #include <stdlib.h>
 
 #include <atomic>
@@ -205,7 +208,97 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
   }
 }
 
-// Row-streaming GEMV on the vector ALUs for M <= MM (MM <= 8).  A wave owns
+// Short-K GEMV with x held in registers, for M <= 16 and K <= 32 * NX
+// (fp16; int8: K <= 32 * NX as well, two fragments per 64-k step).  Every
+// wave loads the B fragments of x for the whole K once, then streams whole
+// 16-row weight tiles: no K split, no LDS, no reduction, one MFMA chain per
+// tile.  Waves stride over the tiles (persistent), so x is loaded once per
+// wave however many tiles it covers.  Loads are issued U steps at a time.
+template <bool I8, int NX, int U>
+__global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
+  constexpr int KSTEP = I8 ? 64 : 32;  // k per weight load step
+  constexpr int NS = I8 ? NX / 2 : NX;  // max weight load steps per tile
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int esz = I8 ? 1 : 2;
+  const int nsteps = (a.K + KSTEP - 1) / KSTEP;
+  const int tiles = (a.N + 15) / 16;
+
+  // x fragments: fp16 step s covers k = 32 s + 8 kq + [0, 8); int8 step s
+  // covers k = 64 s + 16 kq + [0, 16) as fragments 2s and 2s + 1
+  const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
+  const bool mok = r16 < a.M;
+  const uint32_t xbase = (uint32_t)(r16 * a.ldx * 2);
+  int4v xv[NX];
+#pragma unroll
+  for (int f = 0; f < NX; ++f) {
+    const int k = I8 ? (f / 2) * 64 + kq * 16 + (f & 1) * 8 : f * 32 + kq * 8;
+    xv[f] = load16(rX, (mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
+  }
+
+  for (int tile = blockIdx.x * 4 + w; tile < tiles; tile += gridDim.x * 4) {
+    const int n0 = tile * 16;
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
+    const bool rowok = n0 + r16 < a.N;
+    const uint32_t wrow = (uint32_t)(r16 * a.ldw * esz);
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += U) {
+      if (s0 >= nsteps) break;
+      int4v wv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int s = s0 + u;
+        const int k = s * KSTEP + kq * (KSTEP / 4);
+        wv[u] = load16(rW, (s < NS && rowok && k < a.K) ? wrow + (uint32_t)(k * esz) : kOOB);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int s = s0 + u;
+        if (s < NS) {
+          if constexpr (I8) {
+            acc = mfma16(dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]), __builtin_bit_cast(short8v, xv[2 * s]),
+                         acc);
+            acc = mfma16(dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]),
+                         __builtin_bit_cast(short8v, xv[2 * s + 1]), acc);
+          } else {
+            acc = mfma16(__builtin_bit_cast(short8v, wv[u]), __builtin_bit_cast(short8v, xv[s]), acc);
+          }
+        }
+      }
+    }
+    // D[n][m]: lane holds m = lane % 16, n = 4*(lane / 16) + 0..3
+    const int m = lane & 15;
+    const int n = n0 + 4 * (lane >> 4);
+    if (m < a.M && n < a.N) {
+      float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+      if (I8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] *= (float)((const _Float16*)a.scale)[n + q];
+      }
+      if (a.bias) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] += (float)((const _Float16*)a.bias)[n + q];
+      }
+      _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+      *(short4v*)(a.y + ((int64_t)m * a.ldy + n) * 2) = __builtin_bit_cast(short4v, h);
+    }
+  }
+}
+
+template <bool I8>
+hipError_t launch_xreg(const VArgs& v, hipStream_t stream) {
+  const int tiles = (v.N + 15) / 16;
+  int blocks = (tiles + 3) / 4;
+  int cap = 512;  // two 4-wave workgroups per CU: each wave covers several tiles
+  if (const char* e = getenv("HXMI_GEMV_XREG_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL((gemv_xreg<I8, 32, I8 ? 16 : 14>), dim3(blocks), dim3(256), 0, stream, v);
+  return hipGetLastError();
+}
+
+// Row-streaming GEMV on the vector ALUs for M <= MM (MM <= 16).  A wave owns
 // groups of 8 weight rows; lane l covers row l / 8 and the 16-byte chunk
 // l % 8 of every 128-byte K-step (8 k for fp16 weights, 16 for int8), so one
 // wave load is 8 rows x 128 contiguous bytes.  x (M x K, zero-padded to whole
@@ -283,15 +376,18 @@ __global__ __launch_bounds__(256) void gemv_valu(VArgs a, int kpad) {
       acc[m] += __shfl_xor(acc[m], 2, 64);
       acc[m] += __shfl_xor(acc[m], 4, 64);
     }
-    // lane c writes output row m = c
-    float v = 0.f;
+    // lane c writes output rows m = c, c + 8
 #pragma unroll
-    for (int m = 0; m < MM; ++m)
-      if (c == m) v = acc[m];
-    if (rok && c < M) {
-      if (I8) v *= (float)((const _Float16*)a.scale)[row];
-      if (a.bias) v += (float)((const _Float16*)a.bias)[row];
-      ((_Float16*)a.y)[(int64_t)c * a.ldy + row] = (_Float16)v;
+    for (int m0 = 0; m0 < MM; m0 += 8) {
+      float v = 0.f;
+#pragma unroll
+      for (int m = m0; m < MM && m < m0 + 8; ++m)
+        if (c == m - m0) v = acc[m];
+      if (rok && m0 + c < M) {
+        if (I8) v *= (float)((const _Float16*)a.scale)[row];
+        if (a.bias) v += (float)((const _Float16*)a.bias)[row];
+        ((_Float16*)a.y)[(int64_t)(m0 + c) * a.ldy + row] = (_Float16)v;
+      }
     }
   }
 }
@@ -314,7 +410,8 @@ hipError_t launch_valu_sel(const VArgs& v, hipStream_t stream) {
   if (v.M == 1) return launch_valu<1, I8>(v, stream);
   if (v.M == 2) return launch_valu<2, I8>(v, stream);
   if (v.M <= 4) return launch_valu<4, I8>(v, stream);
-  return launch_valu<8, I8>(v, stream);
+  if (v.M <= 8) return launch_valu<8, I8>(v, stream);
+  return launch_valu<16, I8>(v, stream);
 }
 
 template <int TPB, int KS, bool I8>
@@ -367,7 +464,7 @@ hipError_t launch_sel(int tpb, int ks, const VArgs& v, hipStream_t stream) {
 // K groups across workgroups (kg).
 struct GemvPlan {
   int tpb = 1, ks = 8, kg = 1;
-  bool valu = false;
+  bool valu = false, xreg = false;
 };
 
 static GemvPlan gemv_plan(const GemvProblem& p) {
@@ -392,10 +489,17 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   // from N = 4096; the MFMA tiles win where K must be split across waves)
   const int kstep_v = p.w_int8 ? 128 : 64;
   const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
-  const bool fits = p.M <= 8 && p.M * kpad * 2 <= 64 * 1024;
-  g.valu = fits && (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
-  if (const char* e = getenv("HXMI_GEMV_PATH")) g.valu = (e[0] == 'v') && fits;
-  if (g.valu) return g;
+  const bool fits = p.M <= 16 && p.M * kpad * 2 <= 64 * 1024;
+  g.valu = fits && p.M <= 8 && (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
+  // x in registers (K <= 1024): long weight matrices that the row-streaming
+  // kernel does not take
+  const bool xfits = p.K <= 1024;
+  g.xreg = !g.valu && xfits && tiles16 >= 2048;
+  if (const char* e = getenv("HXMI_GEMV_PATH")) {
+    g.valu = (e[0] == 'v') && fits;
+    g.xreg = (e[0] == 'x') && xfits;
+  }
+  if (g.valu || g.xreg) return g;
   // few row groups, each streaming a long K (e.g. a down projection
   // 4864 -> 896): split K over 2-4 workgroups per row group.  Combining the
   // partial tiles costs ~2 us of round trips to memory, so (measured on the
@@ -416,7 +520,7 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
 
 int64_t gemv_workspace_bytes(const GemvProblem& p) {
   const GemvPlan g = gemv_plan(p);
-  if (g.valu || g.kg <= 1) return 0;
+  if (g.valu || g.xreg || g.kg <= 1) return 0;
   const int64_t tiles = (p.N + g.tpb * 16 - 1) / (g.tpb * 16) * g.tpb;  // 16-row tiles of whole row groups
   return gemv_counter_bytes(tiles) + tiles * g.kg * 1024;
 }
@@ -440,6 +544,7 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.epoch = 0;
   const GemvPlan g = gemv_plan(p);
   if (g.valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
+  if (g.xreg) return p.w_int8 ? launch_xreg<true>(v, stream) : launch_xreg<false>(v, stream);
   if (g.kg > 1 && p.ws && p.ws_bytes >= gemv_workspace_bytes(p) && ((uintptr_t)p.ws % 256) == 0) {
     static std::atomic<unsigned long long> calls{1};
     v.kg = g.kg;

@@ -62,12 +62,13 @@ int hxmi_version(void);
  * columns [32q, 32q+16) are gate rows 16q..16q+15 and [32q+16, 32q+32) the
  * matching up rows; C receives N/2 columns, C[:, 16q+i] = silu(g_i) * u_i.
  * bias (fp16, N entries) is required for the BIAS epilogues, else ignored.
- * workspace / workspace_bytes: optional caller-owned device scratch (16-byte
+ * workspace / workspace_bytes: optional caller-owned device scratch (256-byte
  * aligned).  When the output has too few tiles to occupy the GPU and K is
- * long, the GEMM splits K into slices that write fp32 partial sums there and
- * a second kernel reduces them and applies the epilogue; it needs
- * hxmi_gemm_workspace_bytes() bytes.  NULL / 0 (or a smaller buffer) runs
- * the GEMM unsplit.  Two calls must not share a workspace concurrently.
+ * long, the GEMM splits K into slices that write fp32 partial tiles there;
+ * the last slice to finish an output tile adds them in slice order and
+ * applies the epilogue (one launch).  It needs hxmi_gemm_workspace_bytes()
+ * bytes.  NULL / 0 (or a smaller or misaligned buffer) runs the GEMM
+ * unsplit.  Two calls must not share a workspace concurrently.
  * Replaces: the linalg.matmul / matmul_transpose_b lowering scheduled by
  * ScheduleMatmulForHVXPass.cpp:69-195 and tiled by VTCMTiling.cpp:231-266
  * (with HexmemCpyToDMA.cpp:120-271 DMA staging), plus the elementwise

@@ -111,7 +111,7 @@ def test_workspace_queries(pkg):
     lib = pkg.load_library()
     # TinyLlama down projection: 64 tiles of 128x128 -> split K
     need = lib.hxmi_gemm_workspace_bytes(512, 2048, 5632, 1, 0)
-    assert need > 0 and need % (512 * 2048 * 4) == 0
+    assert need > 2 * 512 * 2048 * 4  # >= 2 fp32 partial outputs + arrival counters
     # 4096^3 fills the GPU without splitting; batched / short-K never split
     assert lib.hxmi_gemm_workspace_bytes(4096, 4096, 4096, 1, 0) == 0
     assert lib.hxmi_gemm_workspace_bytes(512, 2048, 512, 1, 0) == 0

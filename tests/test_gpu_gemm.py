@@ -206,6 +206,79 @@ def test_gemm_split_k_epilogues(pkg, dev, force_splits, epi):
     assert ref.max_rel_err(np32(c), exp) <= TOL
 
 
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_gemm_split_k_every_tile_exact(pkg, dev, force_tile, force_splits, tile, layout):
+    # integer-valued operands: every partial tile and their fp32 sum are
+    # exact, so the fixed-up output must equal the rounded exact product
+    force_tile(tile)
+    force_splits(3)
+    M, N, K = 300, 264, 2112
+    a = torch.randint(-2, 3, (M, K), generator=torch.Generator().manual_seed(40)).half()
+    b = torch.randint(-2, 3, (K, N) if layout == "nn" else (N, K), generator=torch.Generator().manual_seed(41)).half()
+    c = run_gemm(pkg, dev, a, b, layout)
+    assert np.array_equal(c.numpy(), f16_round(ref.matmul(a.numpy(), b.numpy(), layout))), f"tile {tile}"
+
+
+def test_gemm_split_k_bf16(pkg, dev, force_splits):
+    force_splits(4)
+    M, N, K = 256, 384, 4096
+    a = normal((M, K), 42, dtype=torch.bfloat16)
+    w = normal((N, K), 43, 0.02, dtype=torch.bfloat16)
+    c = run_gemm(pkg, dev, a, w, "nt")
+    assert ref.max_rel_err(np32(c), ref.linear(np32(a), np32(w))) <= TOL
+
+
+def test_gemm_split_k_deterministic_graph_replays(pkg, dev, force_splits):
+    """The last slice to arrive adds the partial tiles in slice order, so
+    repeated calls are bit-identical; the arrival counters reset themselves,
+    so graph replays with eager calls on the same workspace between them
+    match too, and one workspace serves two shapes back to back."""
+    force_splits(4)
+    lib = pkg.load_library()
+    shapes = [(512, 2048, 5632), (200, 640, 4096)]
+    nbytes = max(lib.hxmi_gemm_workspace_bytes(M, N, K, 1, 0) for M, N, K in shapes)
+    assert nbytes > 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ops = []
+    for i, (M, N, K) in enumerate(shapes):
+        x = normal((M, K), 44 + i).to(dev)
+        w = normal((N, K), 46 + i, 0.02).to(dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        ops.append((x, w, y, M, N, K))
+
+    def call(op, stream):
+        x, w, y, M, N, K = op
+        rc = lib.hxmi_gemm_f16(x.data_ptr(), w.data_ptr(), y.data_ptr(), None, M, N, K, K, K, N, 1, 0, 1.0,
+                               ws.data_ptr(), nbytes, stream)
+        assert rc == 0, lib.hxmi_last_error()
+
+    eager = []
+    for op in ops:
+        call(op, None)
+        torch.cuda.synchronize()
+        eager.append(op[2].clone())
+        exp = ref.linear(op[0].cpu().numpy(), op[1].cpu().numpy())
+        assert ref.max_rel_err(np32(op[2].cpu()), exp) <= TOL
+    for op, e in zip(ops, eager):
+        call(op, None)
+        torch.cuda.synchronize()
+        assert torch.equal(op[2], e)
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(ops[0], s.cuda_stream)
+    for _ in range(3):
+        ops[0][2].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ops[0][2], eager[0])
+        call(ops[1], None)  # another shape on the same workspace between replays
+        torch.cuda.synchronize()
+        assert torch.equal(ops[1][2], eager[1])
+
+
 def test_gemm_split_k_default_down_projection(pkg, dev):
     # TinyLlama down projection: the dispatcher splits K by itself
     assert pkg.load_library().hxmi_gemm_workspace_bytes(512, 2048, 5632, 1, 0) > 0

@@ -68,7 +68,8 @@ def test_w8a16_qwen_shapes(pkg, dev, M, K, N):
 
 @pytest.fixture
 def gemv_path(monkeypatch):
-    """Force the decode kernel: "mfma" (16-row MFMA tiles) or "valu" (row streaming)."""
+    """Force the decode kernel: "mfma" (16-row MFMA tiles, K split over
+    waves), "valu" (row streaming) or "xreg" (x in registers, K <= 1024)."""
 
     def force(path):
         monkeypatch.setenv("HXMI_GEMV_PATH", path)
@@ -76,7 +77,7 @@ def gemv_path(monkeypatch):
     return force
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("path", ["mfma", "valu", "xreg"])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("N,K", [(4100, 904), (1028, 136), (8, 64)])
 def test_gemv_both_paths(pkg, dev, gemv_path, path, M, N, K):
@@ -89,7 +90,7 @@ def test_gemv_both_paths(pkg, dev, gemv_path, path, M, N, K):
     assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("path", ["mfma", "valu", "xreg"])
 @pytest.mark.parametrize("M", [1, 3, 8])
 @pytest.mark.parametrize("N,K", [(4104, 912), (264, 144)])
 def test_w8a16_both_paths(pkg, dev, gemv_path, path, M, N, K):
@@ -102,7 +103,7 @@ def test_w8a16_both_paths(pkg, dev, gemv_path, path, M, N, K):
     assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("path", ["mfma", "valu", "xreg"])
 def test_w8a16_onehot_exact_both_paths(pkg, dev, gemv_path, path):
     gemv_path(path)
     d = np.load(GOLDEN / "w8_onehot.npz")
@@ -259,3 +260,41 @@ def test_gemv_k_groups_graph_replays(pkg, dev):
         call(None)  # eager call between replays, same workspace
         torch.cuda.synchronize()
         assert torch.equal(y, eager)
+
+
+@pytest.mark.parametrize("M", [1, 7, 16])
+@pytest.mark.parametrize("N,K", [(2056, 1024), (40, 8), (300, 520), (33000, 896)])
+def test_gemv_xreg(pkg, dev, gemv_path, M, N, K):
+    # x held in registers for the whole K: K up to 1024, ragged K steps and
+    # row tiles, more tiles than waves (each wave strides over several)
+    gemv_path("xreg")
+    x = normal((M, K), 71 + M)
+    w = normal((N, K), 72, 0.05)
+    b = normal((N,), 73)
+    y = pkg.gemv(x.to(dev), w.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("N,K", [(2056, 1024), (24, 16), (33000, 896)])
+def test_w8a16_xreg(pkg, dev, gemv_path, M, N, K):
+    gemv_path("xreg")
+    x = normal((M, K), 81 + M)
+    q, s = int8_weights(N, K, 82)
+    b = normal((N,), 83)
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("M", [9, 16])
+@pytest.mark.parametrize("N,K", [(2056, 1024), (40, 8), (33000, 896)])
+def test_gemv_valu_two_row_blocks(pkg, dev, gemv_path, M, N, K):
+    # M > 8 on the row-streaming kernel: lanes write rows c and c + 8
+    gemv_path("valu")
+    x = normal((M, K), 91 + M)
+    w = normal((N, K), 92, 0.05)
+    y = pkg.gemv(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy())) <= TOL
