@@ -38,7 +38,8 @@ int from_hip(hipError_t e, const char* what) {
 int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bias, int64_t batch, int64_t M,
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC,
                 int b_is_nt, int epilogue, float alpha, int out_f32, void* ws, int64_t ws_bytes, void* stream,
-                const char* name, int rms = 0, float rms_eps = 0.f) {
+                const char* name, int rms = 0, float rms_eps = 0.f, float* rs_out = nullptr,
+                const float* rs_in = nullptr) {
   REQUIRE(batch >= 0 && M >= 0 && N >= 0 && K >= 0, "%s: negative size (batch=%lld M=%lld N=%lld K=%lld)", name,
           (long long)batch, (long long)M, (long long)N, (long long)K);
   REQUIRE(b_is_nt == 0 || b_is_nt == 1, "%s: b_is_nt must be 0 or 1", name);
@@ -79,6 +80,8 @@ int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bi
   p.ws_bytes = ws_bytes > 0 ? ws_bytes : 0;
   p.rms = rms;
   p.rms_eps = rms_eps;
+  p.rs_out = rs_out;
+  p.rs_in = rs_in;
   return from_hip(hxmi::launch_gemm(p, (hipStream_t)stream), name);
 }
 
@@ -313,14 +316,19 @@ int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int
 }
 
 int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, int64_t M, int64_t N, int64_t K, int64_t ldx,
-                            int64_t ldw, int64_t ldc, int epilogue, float eps, void* stream) {
+                            int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
+                            const float* rscale_in, void* stream) {
   const char* name = "hxmi_rmsnorm_linear_f16";
   REQUIRE(epilogue == HXMI_EPI_NONE || epilogue == HXMI_EPI_SILU_MUL, "%s: epilogue %d unsupported (none or silu_mul)",
           name, epilogue);
   REQUIRE(K > 0 || M <= 0 || N <= 0, "%s: RMSNorm over zero columns", name);
   REQUIRE(eps >= 0.f, "%s: negative eps", name);
+  REQUIRE(!(rscale_out && rscale_in), "%s: rscale_out and rscale_in are exclusive", name);
+  if (rscale_in)  // statistics given: a plain GEMM with a row scale before the epilogue
+    return gemm_common(hxmi::DT_F16, x, Wg, C, nullptr, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0,
+                       nullptr, 0, stream, name, 0, 0.f, nullptr, rscale_in);
   return gemm_common(hxmi::DT_F16, x, Wg, C, nullptr, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr,
-                     0, stream, name, 1, eps);
+                     0, stream, name, 1, eps, rscale_out, nullptr);
 }
 
 int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,

@@ -26,6 +26,8 @@ struct GArgs {
   int nn, epi, out_f32;
   int rms;  // scale each output row by rsqrt(mean(A[m,:]^2) + rms_eps)
   float rms_eps;
+  float* rs_out;       // rms: the row scales, written by the column-0 threads
+  const float* rs_in;  // !rms: given row scales
 };
 
 template <typename T>
@@ -67,6 +69,10 @@ __global__ __launch_bounds__(256) void gemm_elementwise(GArgs a) {
     const float r = rsqrtf(ss / (float)a.K + a.rms_eps);
     acc0 *= r;
     acc1 *= r;
+    if (a.rs_out && o == 0) a.rs_out[m] = r;
+  } else if (a.rs_in) {
+    acc0 *= a.rs_in[m];
+    acc1 *= a.rs_in[m];
   }
   float v = acc0 * a.alpha;
   if (a.epi == EPI_SILU_MUL) {
@@ -175,6 +181,8 @@ KArgs make_kargs(const GemmProblem& p, int tile) {
   k.group_m = gm < 1 ? 1 : (gm > k.tiles_m ? k.tiles_m : gm);
   k.k_last = 0;
   k.rms_eps = p.rms_eps;
+  k.rs_out = p.rs_out;
+  k.rs_in = p.rs_in;
   return k;
 }
 
@@ -262,6 +270,8 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream) {
     g.out_f32 = p.out_f32;
     g.rms = p.rms;
     g.rms_eps = p.rms_eps;
+    g.rs_out = p.rs_out;
+    g.rs_in = p.rs_in;
     const int64_t total = p.batch * p.M * g.Nout;
     const int64_t blocks = (total + 255) / 256;
     if (blocks >= (1ll << 31)) return hipErrorInvalidValue;

@@ -49,6 +49,8 @@ struct KArgs {
   // epoch tags the call so counters left by other calls read as zero.
   char* fix;
   unsigned long long epoch;
+  float* rs_out;       // RMS kernels: row scales rsqrt(mean + eps) written here (optional)
+  const float* rs_in;  // other kernels: row scales applied before the epilogue (optional)
 };
 
 // Bytes of the arrival counters at the head of a split-K fix-up workspace.
@@ -519,6 +521,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       const float r = rsqrtf(tot / (float)a.K + a.rms_eps);
 #pragma unroll
       for (int i = 0; i < TN; ++i) acc[i][j] *= r;
+      // the first column of tiles publishes the row scales for other
+      // consumers of the same normalised rows
+      const int m = m0 + wm * WM + j * 32 + lane;
+      if (a.rs_out && tn == 0 && wn == 0 && lane < 32 && m < a.M) a.rs_out[m] = r;
     }
   }
 
@@ -577,6 +583,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
               for (int q = 0; q < 4; ++q) acc[i][j][4 * g + q] = sl == 0 ? v[q] : acc[i][j][4 * g + q] + v[q];
             }
+      }
+    }
+  }
+
+  if constexpr (!RMS) {
+    if (a.rs_in) {
+      // rows normalised by scales another GEMM computed (B holds the folded
+      // norm weight)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int m = m0 + wm * WM + j * 32 + (lane & 31);
+        const float r = m < a.M ? a.rs_in[m] : 0.f;
+#pragma unroll
+        for (int i = 0; i < TN; ++i) acc[i][j] *= r;
       }
     }
   }

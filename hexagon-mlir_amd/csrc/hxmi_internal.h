@@ -43,6 +43,8 @@ struct GemmProblem {
   const void* scale;  // int8 B only: per-column fp16 scale
   int rms;            // 1: C = epilogue(rmsnorm(A) . B^T), B holds the folded norm weight
   float rms_eps;
+  float* rs_out;       // rms: also write each row's rsqrt(mean(A[m,:]^2) + eps) here
+  const float* rs_in;  // !rms: scale row m of A . B^T by rs_in[m] before the epilogue
 };
 
 // Wg[n][k] = fp16(W[n][k] * g[k]): folds an RMSNorm weight into the linear

@@ -46,7 +46,7 @@ SIGNATURES = {
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
-    "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P], _I),
+    "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
 }
@@ -273,10 +273,19 @@ def fold_rms_weight(w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
 
 
 def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, epilogue: Optional[str] = None,
-                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    out: Optional[torch.Tensor] = None, rscale_out: Optional[torch.Tensor] = None,
+                    rscale_in: Optional[torch.Tensor] = None) -> torch.Tensor:
     """linear(rms_norm(x, g, eps), w) in one GEMM, with w_folded = fold_rms_weight(w, g);
-    epilogue None or "silu_mul" (w packed by pack_gate_up before folding)."""
-    _require_gpu(x, w_folded, out)
+    epilogue None or "silu_mul" (w packed by pack_gate_up before folding).
+
+    rscale_out (fp32, one per row of x) also receives the row scales
+    rsqrt(mean(x^2) + eps); a later call on the same x can pass them as
+    rscale_in and skip the statistics (eps is then ignored)."""
+    _require_gpu(x, w_folded, out, rscale_out, rscale_in)
+    if rscale_out is not None and rscale_in is not None:
+        raise HxmiError("rscale_out and rscale_in are exclusive")
+    if rscale_out is not None and not rscale_out.is_contiguous():
+        raise HxmiError("rscale_out must be contiguous")
     if x.dtype != torch.float16 or w_folded.dtype != torch.float16:
         raise HxmiError("rms_norm_linear takes fp16 tensors")
     if epilogue not in (None, "silu_mul"):
@@ -291,9 +300,12 @@ def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, 
     if out is None:
         out = torch.empty((M, nout), dtype=x.dtype, device=x.device)
     out2 = out.reshape(M, nout)
+    rs_out = _vec(rscale_out, M, torch.float32, "rscale_out")
+    rs_in = _vec(rscale_in, M, torch.float32, "rscale_in")
     _check(load_library().hxmi_rmsnorm_linear_f16(x2.data_ptr(), w_folded.data_ptr(), out2.data_ptr(), M, N, K,
                                                   _rowmajor(x2, "x"), _rowmajor(w_folded, "w"), _rowmajor(out2, "out"),
-                                                  EPILOGUES[epilogue], float(eps), _stream(x)))
+                                                  EPILOGUES[epilogue], float(eps), _ptr(rs_out), _ptr(rs_in),
+                                                  _stream(x)))
     return out2.reshape(*lead, nout)
 
 

@@ -170,13 +170,20 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
  * or HXMI_EPI_SILU_MUL (packed gate/up Wg, as hxmi_gemm_f16; N' = N/2).
  * fp32 statistics and accumulation; differs from normalise-round-multiply
  * (HF LlamaRMSNorm) by the fp16 rounding of the normalised activations.
+ * rscale_out (optional, M floats): also receives each row's
+ * rsqrt(mean_k x[m,k]^2 + eps).  rscale_in (optional, M floats): row scales
+ * a previous call computed for the same x; the statistics are then not
+ * recomputed (eps is ignored) and C = epilogue(diag(rscale_in) . x . Wg^T),
+ * so a second consumer of the same normalised rows (the gate/up projection
+ * beside QKV) costs a plain GEMM.  The two are exclusive.
  * Replaces: the RMSNorm generic chain (SplitReductionUtils.cpp,
  * TilingPass.cpp:261-289; semantics test/python/triton/test_rms_norm.py:37-63)
  * plus the matmul_transpose_b after it (ScheduleMatmulForHVXPass.cpp:69-195),
  * which the reference runs as separate passes over HBM.
  */
 int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, int64_t M, int64_t N, int64_t K, int64_t ldx,
-                            int64_t ldw, int64_t ldc, int epilogue, float eps, void* stream);
+                            int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
+                            const float* rscale_in, void* stream);
 
 /* Wg[n,k] = fp16(W[n,k] * g[k]) (fp32 product, one rounding): the weight
  * hxmi_rmsnorm_linear_f16 takes.  W, Wg [N,K] (leading dims ldw, ldwg), g [K]. */

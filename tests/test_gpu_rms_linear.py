@@ -121,5 +121,60 @@ def test_rms_norm_linear_rejects_bias_epilogue(pkg, dev):
     lib = pkg.load_library()
     t = torch.zeros(64, 64, dtype=torch.float16, device=dev)
     rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), 64, 64, 64, 64, 64, 64, 1,
-                                     ctypes.c_float(1e-5), None)
+                                     ctypes.c_float(1e-5), None, None, None)
     assert rc == 1 and b"epilogue" in lib.hxmi_last_error()
+    r = torch.zeros(64, dtype=torch.float32, device=dev)
+    rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), 64, 64, 64, 64, 64, 64, 0,
+                                     ctypes.c_float(1e-5), r.data_ptr(), r.data_ptr(), None)
+    assert rc == 1 and b"exclusive" in lib.hxmi_last_error()
+
+
+def _rscale(x, eps):
+    xf = np32(x).astype(np.float64)
+    return (1.0 / np.sqrt((xf * xf).mean(axis=1) + eps)).astype(np.float32)
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_rscale_out_every_tile(pkg, dev, force_tile, tile):
+    # the first column of tiles writes each row's rsqrt(mean(x^2) + eps)
+    force_tile(tile)
+    M, N, K = 300, 256, 520
+    x = normal((M, K), 21)
+    wf = pkg.fold_rms_weight(normal((N, K), 22, 0.05).to(dev), _norm_weight(K, 23).to(dev))
+    rs = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    pkg.rms_norm_linear(x.to(dev), wf, 1e-5, rscale_out=rs)
+    assert np.allclose(rs.cpu().numpy(), _rscale(x, 1e-5), rtol=1e-5, atol=0)
+
+
+def test_rscale_out_elementwise_path(pkg, dev):
+    M, N, K = 33, 72, 1000 + 3  # K % 8 != 0: element-wise kernel
+    x = normal((M, K), 24)
+    wf = pkg.fold_rms_weight(normal((N, K), 25, 0.05).to(dev), _norm_weight(K, 26).to(dev))
+    rs = torch.full((M,), -1.0, dtype=torch.float32, device=dev)
+    pkg.rms_norm_linear(x.to(dev), wf, 1e-6, rscale_out=rs)
+    assert np.allclose(rs.cpu().numpy(), _rscale(x, 1e-6), rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("tile", [None, 4, 11, 13])
+@pytest.mark.parametrize("M,K", [(512, 2048), (200, 264), (7, 1003)])
+def test_rscale_in_second_consumer(pkg, dev, force_tile, tile, M, K):
+    """QKV computes the row scales, gate/up (SiLU-mul) reuses them: same
+    result as recomputing the statistics, against the exact oracle."""
+    if tile is not None:
+        force_tile(tile)
+    I = 160
+    x = normal((M, K), 27)
+    g = _norm_weight(K, 28)
+    wq = normal((96, K), 29, 0.05)
+    wg, wu = normal((I, K), 30, 0.05), normal((I, K), 31, 0.05)
+    xd = x.to(dev)
+    wqf = pkg.fold_rms_weight(wq.to(dev), g.to(dev))
+    wguf = pkg.fold_rms_weight(pkg.pack_gate_up(wg.to(dev), wu.to(dev)), g.to(dev))
+    rs = torch.empty(M, dtype=torch.float32, device=dev)
+    q = pkg.rms_norm_linear(xd, wqf, 1e-5, rscale_out=rs).cpu()
+    h = pkg.rms_norm_linear(xd, wguf, 1e-5, epilogue="silu_mul", rscale_in=rs).cpu()
+    h_rms = pkg.rms_norm_linear(xd, wguf, 1e-5, epilogue="silu_mul").cpu()
+    xn = ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-5)
+    check(q, x, wqf.cpu(), ref.linear(xn, wq.numpy()), 1e-5)
+    check(h, x, wguf.cpu(), ref.silu_mul_linear(xn, wg.numpy(), wu.numpy()), 1e-5, "silu_mul")
+    assert ref.max_rel_err(np32(h), np32(h_rms)) <= 1e-3
