@@ -130,14 +130,21 @@ int gemm_pick_tile(const GemmProblem& p) {
   const int cus = 256;
   int best = TILE_64x64;
   double best_t = 1e300;
+  const bool i8 = p.dtype == DT_W8A16;
   for (const Cand& c : cands) {
     if (c.bn == 64 && p.epilogue == EPI_SILU_MUL) continue;
+    // int8 B converts every weight once per tile row: tall tiles amortise
+    // it, and the latency-bound small shapes want the most workgroups
+    // (measured on the Qwen2.5-0.5B int8 shapes at M = 256)
+    float eff = c.eff;
+    if (i8 && (c.id == TILE_128x128_W8 || c.id == TILE_256x128_W8)) eff = 0.80f;
+    if (i8 && c.id == TILE_64x64) eff = 0.60f;
     const int64_t tm = (p.M + c.bm - 1) / c.bm, tn = (p.N + c.bn - 1) / c.bn;
     const int64_t tiles = tm * tn * p.batch;
     const int64_t slots = (int64_t)cus * c.per_cu;
     const int64_t rounds = (tiles + slots - 1) / slots;
     const int64_t conc = tiles < slots ? (tiles + cus - 1) / cus : c.per_cu;  // tiles sharing a CU
-    const double t = (double)rounds * c.bm * c.bn * (double)(conc > 0 ? conc : 1) / c.eff;
+    const double t = (double)rounds * c.bm * c.bn * (double)(conc > 0 ? conc : 1) / eff;
     if (t < best_t * 0.999) {
       best_t = t;
       best = c.id;
@@ -204,6 +211,8 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 // TinyLlama down projection (512x2048x5632: 431 -> 464 TFLOP/s against
 // 128x128 tiles) and ViT-B/16 fc2 (1576x768x3072: 316 -> 376); with K below
 // 3072 (the 512-token QKV and O projections) every split measured slower.
+// With int8 weights the slices run 64x64 tiles (Qwen2.5-0.5B down
+// projection at M = 256: 105 -> 128 TFLOP/s).
 int gemm_splits(const GemmProblem& p) {
   if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || !gemm_fast_path_ok(p)) return 1;
   if (const char* e = getenv("HXMI_SPLITK")) return atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
@@ -228,7 +237,7 @@ static bool split_plan(const GemmProblem& p, GemmProblem& q, int& tile, int64_t&
   q.sA = kc;
   q.sB = p.b_nt ? kc : kc * p.ldb;
   q.sC = 0;
-  if (q.tile < 0 && gemm::env_int("HXMI_GEMM_TILE", -1) < 0) q.tile = TILE_64x128;
+  if (q.tile < 0 && gemm::env_int("HXMI_GEMM_TILE", -1) < 0) q.tile = p.dtype == DT_W8A16 ? TILE_64x64 : TILE_64x128;
   tile = gemm::tile_for(q);
   const gemm::TileShape s = gemm::kTiles[tile];
   const int64_t tiles = ((p.M + s.BM - 1) / s.BM) * ((p.N + s.BN - 1) / s.BN);
