@@ -14,6 +14,12 @@ in the plan):
   rms_norm       aten.rms_norm, or the HF LlamaRMSNorm chain
                  to(f32) -> pow 2 -> mean(-1) -> add eps -> rsqrt -> mul ->
                  to(dtype) -> mul weight
+  rms_linear     an fp16 RMSNorm whose every user is a linear layer (q/k/v,
+                 with or without bias) or a fused gate/up: the norm weight is
+                 folded into each weight, the first projection takes the row
+                 statistics inside its GEMM and publishes the row scales, the
+                 others reuse them (no RMSNorm kernel, the normalised
+                 activations never go to memory)
   silu_mul       mul(silu(linear(h, Wg)), linear(h, Wu)) -> one GEMM over the
                  packed gate/up weight with the SiLU-mul epilogue
   linear_gelu    gelu(linear(x, W, b), approximate="tanh") -> GEMM + epilogue
@@ -24,6 +30,7 @@ in the plan):
 from __future__ import annotations
 
 import math
+import operator
 from dataclasses import dataclass, field
 from typing import Any, Optional
 
@@ -53,6 +60,22 @@ def hx_linear(x, w, b=None, act=None):
 
 def hx_silu_mul_linear(x, w_packed):
     return _pkg().linear(x, w_packed, epilogue="silu_mul")
+
+
+def hx_rms_linear_group(x, eps, specs):
+    """The projections of one RMSNorm: specs = ((w_folded, bias, epilogue), ...).
+    The first takes the row statistics and publishes the row scales; the
+    others apply them.  Returns one output per spec."""
+    pkg = _pkg()
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    rs = torch.empty(x2.shape[0], dtype=torch.float32, device=x.device)
+    outs = []
+    for i, (w, b, epi) in enumerate(specs):
+        rsk = {"rscale_out": rs} if i == 0 else {"rscale_in": rs}
+        y = pkg.rms_norm_linear(x2, w, eps, epilogue=epi, bias=b, **rsk)
+        outs.append(y.reshape(*lead, y.shape[-1]))
+    return tuple(outs)
 
 
 def _as_nt(b):
@@ -140,6 +163,8 @@ class _Planner:
         self.fusion = fusion
         self.plan = Plan(gm)
         self._packed = 0
+        self._entry = {}  # rewritten node -> its index in plan.kernels
+        self._dropped = set()  # plan.kernels entries whose kernel a later fusion removed
 
     def replace(self, old: fx.Node, fn, args, pattern: str):
         with self.g.inserting_before(old):
@@ -147,8 +172,15 @@ class _Planner:
         new.meta.update(old.meta)
         old.replace_all_uses_with(new)
         self.g.erase_node(old)  # some ops (e.g. SDPA) are not removed by dead-code elimination
+        self._entry[new] = len(self.plan.kernels)
         self.plan.kernels.append((pattern, old.name))
         return new
+
+    def _buffer(self, t: torch.Tensor, stem: str) -> str:
+        name = f"_hxmi_{stem}_{self._packed}"
+        self._packed += 1
+        self.gm.register_buffer(name, t)
+        return name
 
     # -- patterns ----------------------------------------------------------------------
 
@@ -230,6 +262,52 @@ class _Planner:
                 self.replace(m, hx_silu_mul_linear, (g.args[0], pw), "silu_mul")
                 break
 
+    def rms_linear(self):
+        for rn in list(self.g.nodes):
+            if not (rn.op == "call_function" and rn.target is hx_rms_norm):
+                continue
+            x, gw, eps = rn.args
+            g = self._attr(gw)
+            if g is None or _val(x) is None or _val(x).dtype != torch.float16 or not rn.users:
+                continue
+            specs = []  # (consumer, weight, bias, epilogue)
+            for u in rn.users:
+                if u.op == "call_function" and u.target is hx_silu_mul_linear and u.args[0] is rn:
+                    specs.append((u, self._attr(u.args[1]), None, "silu_mul"))
+                elif _is(u, aten.linear.default) and u.args[0] is rn and _is_half(u):
+                    b = u.args[2] if len(u.args) > 2 else None
+                    bt = None if b is None else self._attr(b)
+                    if b is not None and bt is None:
+                        break
+                    specs.append((u, self._attr(u.args[1]), bt, None))
+                else:
+                    break
+                if specs[-1][1] is None:
+                    break
+            else:
+                order = {n: i for i, n in enumerate(self.g.nodes)}
+                specs.sort(key=lambda sp: order[sp[0]])
+                first = specs[0][0]
+                with self.g.inserting_before(first):
+                    args = []
+                    for _, w, bt, epi in specs:
+                        wf = self.g.get_attr(self._buffer(_pkg().fold_rms_weight(w.detach(), g.detach()), "rmsfold"))
+                        bn = None if bt is None else self.g.get_attr(self._buffer(bt.detach().clone(), "bias"))
+                        args.append((wf, bn, epi))
+                    grp = self.g.call_function(hx_rms_linear_group, (x, float(eps), tuple(args)))
+                for i, (u, _, _, epi) in enumerate(specs):
+                    with self.g.inserting_before(u):
+                        item = self.g.call_function(operator.getitem, (grp, i))
+                    item.meta.update(u.meta)
+                    u.replace_all_uses_with(item)
+                    if u in self._entry:
+                        self._dropped.add(self._entry[u])
+                    self.g.erase_node(u)
+                    self.plan.kernels.append(("rms_linear" if epi is None else "rms_silu_mul", u.name))
+                if rn in self._entry:
+                    self._dropped.add(self._entry[rn])
+                self.g.erase_node(rn)
+
     def linear_gelu(self):
         for ge in list(self.g.nodes):
             if not _is(ge, aten.gelu.default):
@@ -301,11 +379,14 @@ class _Planner:
             self.linear_gelu()
             self.attention()
             self.g.eliminate_dead_code()  # drop what the fused patterns replaced
+            self.rms_norm_ops()
+            self.rms_linear()
         self.rms_norm_ops()
         self.single_ops()
         self.g.eliminate_dead_code()
         self.g.lint()
         self.gm.recompile()
+        self.plan.kernels = [k for i, k in enumerate(self.plan.kernels) if i not in self._dropped]
         self.plan.torch_ops = [f"{n.name}: {n.target}" for n in self.g.nodes
                                if n.op == "call_function" and isinstance(n.target, torch._ops.OpOverload)]
         return self.plan

@@ -7,7 +7,9 @@
 // Gimelshein 2018, the blockwise form the reference's
 // test/python/triton/test_online_softmax.py:30-81 exercises):
 //   * a workgroup is 4 waves x 32 queries of one (batch, head); K and V pass
-//     through LDS in chunks of 128 keys shared by the 4 waves;
+//     through LDS in chunks of 256 keys (D = 64; 128 for D = 128: 64 KB
+//     either way) shared by the 4 waves, so a ViT sequence (197 tokens) is
+//     one chunk, loaded with every global load in flight at once;
 //   * S is computed as D[key][query] = K . Q^T with v_mfma_f32_32x32x16_f16,
 //     so every lane owns one query's scores: the row max / sum are in-lane
 //     plus one exchange with the lane 32 away;
@@ -23,7 +25,6 @@
 namespace hxmi {
 namespace {
 
-constexpr int KC = 128;  // keys per LDS chunk
 
 struct AArgs {
   const char* q;
@@ -58,9 +59,11 @@ __device__ __forceinline__ int v_off(int r, int c) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attention_fwd(AArgs a) {
+  constexpr int KC = D == 64 ? 256 : 128;  // keys per LDS chunk (32 KB of K, 32 KB of V)
   constexpr int DC = D / 8;   // 16-byte chunks per row
   constexpr int DS = D / 16;  // 16-deep MFMA steps over the head dim
   constexpr int DT = D / 32;  // 32-wide output tiles over the head dim
+  constexpr int PER = KC * DC / 256;  // 16-byte chunks of K (and of V) per thread
   __shared__ __attribute__((aligned(1024))) char ks[KC * 2 * D];
   __shared__ __attribute__((aligned(1024))) char vs[KC * 2 * D];
 
@@ -91,17 +94,27 @@ __global__ __launch_bounds__(256) void attention_fwd(AArgs a) {
   float m_run = -INFINITY, l_run = 0.f;
 
   for (int c0 = 0; c0 < a.skv; c0 += KC) {
-    __syncthreads();  // previous chunk fully consumed
-    for (int idx = threadIdx.x; idx < KC * DC; idx += 256) {
+    // every load of the chunk in flight before the first LDS store
+    int4v kv[PER], vv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = i * 256 + threadIdx.x;
       const int r = idx / DC, c = idx % DC;
       const int key = c0 + r;
-      int4v kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+      kv[i] = int4v{0, 0, 0, 0};
+      vv[i] = int4v{0, 0, 0, 0};
       if (key < a.skv) {
-        kv = *(const int4v*)(Kp + ((int64_t)key * a.ldk + c * 8) * 2);
-        vv = *(const int4v*)(Vp + ((int64_t)key * a.ldv + c * 8) * 2);
+        kv[i] = *(const int4v*)(Kp + ((int64_t)key * a.ldk + c * 8) * 2);
+        vv[i] = *(const int4v*)(Vp + ((int64_t)key * a.ldv + c * 8) * 2);
       }
-      *(int4v*)(ks + k_off<D>(r, c)) = kv;
-      *(int4v*)(vs + v_off<D>(r, c)) = vv;
+    }
+    __syncthreads();  // previous chunk fully consumed
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = i * 256 + threadIdx.x;
+      const int r = idx / DC, c = idx % DC;
+      *(int4v*)(ks + k_off<D>(r, c)) = kv[i];
+      *(int4v*)(vs + v_off<D>(r, c)) = vv[i];
     }
     __syncthreads();
 

@@ -315,19 +315,19 @@ int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int
   return from_hip(hxmi::launch_attention(p, (hipStream_t)stream), name);
 }
 
-int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, int64_t M, int64_t N, int64_t K, int64_t ldx,
-                            int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
+int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                            int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
                             const float* rscale_in, void* stream) {
   const char* name = "hxmi_rmsnorm_linear_f16";
-  REQUIRE(epilogue == HXMI_EPI_NONE || epilogue == HXMI_EPI_SILU_MUL, "%s: epilogue %d unsupported (none or silu_mul)",
-          name, epilogue);
+  REQUIRE(epilogue == HXMI_EPI_NONE || epilogue == HXMI_EPI_BIAS || epilogue == HXMI_EPI_SILU_MUL,
+          "%s: epilogue %d unsupported (none, bias or silu_mul)", name, epilogue);
   REQUIRE(K > 0 || M <= 0 || N <= 0, "%s: RMSNorm over zero columns", name);
   REQUIRE(eps >= 0.f, "%s: negative eps", name);
   REQUIRE(!(rscale_out && rscale_in), "%s: rscale_out and rscale_in are exclusive", name);
   if (rscale_in)  // statistics given: a plain GEMM with a row scale before the epilogue
-    return gemm_common(hxmi::DT_F16, x, Wg, C, nullptr, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0,
+    return gemm_common(hxmi::DT_F16, x, Wg, C, bias, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0,
                        nullptr, 0, stream, name, 0, 0.f, nullptr, rscale_in);
-  return gemm_common(hxmi::DT_F16, x, Wg, C, nullptr, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr,
+  return gemm_common(hxmi::DT_F16, x, Wg, C, bias, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr,
                      0, stream, name, 1, eps, rscale_out, nullptr);
 }
 

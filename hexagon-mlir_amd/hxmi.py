@@ -46,7 +46,7 @@ SIGNATURES = {
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
-    "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
+    "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
 }
@@ -274,14 +274,14 @@ def fold_rms_weight(w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
 
 def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, epilogue: Optional[str] = None,
                     out: Optional[torch.Tensor] = None, rscale_out: Optional[torch.Tensor] = None,
-                    rscale_in: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """linear(rms_norm(x, g, eps), w) in one GEMM, with w_folded = fold_rms_weight(w, g);
-    epilogue None or "silu_mul" (w packed by pack_gate_up before folding).
+                    rscale_in: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """linear(rms_norm(x, g, eps), w, bias) in one GEMM, with w_folded = fold_rms_weight(w, g);
+    epilogue None or "silu_mul" (w packed by pack_gate_up before folding; no bias).
 
     rscale_out (fp32, one per row of x) also receives the row scales
     rsqrt(mean(x^2) + eps); a later call on the same x can pass them as
     rscale_in and skip the statistics (eps is then ignored)."""
-    _require_gpu(x, w_folded, out, rscale_out, rscale_in)
+    _require_gpu(x, w_folded, out, rscale_out, rscale_in, bias)
     if rscale_out is not None and rscale_in is not None:
         raise HxmiError("rscale_out and rscale_in are exclusive")
     if rscale_out is not None and not rscale_out.is_contiguous():
@@ -290,6 +290,8 @@ def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, 
         raise HxmiError("rms_norm_linear takes fp16 tensors")
     if epilogue not in (None, "silu_mul"):
         raise HxmiError(f"rms_norm_linear epilogue must be None or 'silu_mul', got {epilogue!r}")
+    if bias is not None and epilogue is not None:
+        raise HxmiError("rms_norm_linear takes a bias only without an epilogue")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     M, K = x2.shape
@@ -302,9 +304,11 @@ def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, 
     out2 = out.reshape(M, nout)
     rs_out = _vec(rscale_out, M, torch.float32, "rscale_out")
     rs_in = _vec(rscale_in, M, torch.float32, "rscale_in")
-    _check(load_library().hxmi_rmsnorm_linear_f16(x2.data_ptr(), w_folded.data_ptr(), out2.data_ptr(), M, N, K,
-                                                  _rowmajor(x2, "x"), _rowmajor(w_folded, "w"), _rowmajor(out2, "out"),
-                                                  EPILOGUES[epilogue], float(eps), _ptr(rs_out), _ptr(rs_in),
+    bias = _vec(bias, N, torch.float16, "bias")
+    epi = EPILOGUES["bias"] if bias is not None else EPILOGUES[epilogue]
+    _check(load_library().hxmi_rmsnorm_linear_f16(x2.data_ptr(), w_folded.data_ptr(), out2.data_ptr(), _ptr(bias),
+                                                  M, N, K, _rowmajor(x2, "x"), _rowmajor(w_folded, "w"),
+                                                  _rowmajor(out2, "out"), epi, float(eps), _ptr(rs_out), _ptr(rs_in),
                                                   _stream(x)))
     return out2.reshape(*lead, nout)
 

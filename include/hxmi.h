@@ -166,8 +166,10 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
  *   C[M,N'] = epilogue(rmsnorm(x) . W^T),  rmsnorm(x)[m,k] = x[m,k] * g[k] / sqrt(mean_k x[m,k]^2 + eps)
  * with Wg[N,K] = g (.) W prepared once by hxmi_fold_rmsnorm_weight_f16.  The
  * row statistics are taken inside the GEMM from the x tiles it multiplies,
- * so the normalised activations never go to memory.  epilogue: HXMI_EPI_NONE
- * or HXMI_EPI_SILU_MUL (packed gate/up Wg, as hxmi_gemm_f16; N' = N/2).
+ * so the normalised activations never go to memory.  epilogue: HXMI_EPI_NONE,
+ * HXMI_EPI_BIAS (bias: fp16, N entries, added after the normalisation, as
+ * Qwen2's q/k/v projections) or HXMI_EPI_SILU_MUL (packed gate/up Wg, as
+ * hxmi_gemm_f16; N' = N/2).
  * fp32 statistics and accumulation; differs from normalise-round-multiply
  * (HF LlamaRMSNorm) by the fp16 rounding of the normalised activations.
  * rscale_out (optional, M floats): also receives each row's
@@ -181,8 +183,8 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
  * plus the matmul_transpose_b after it (ScheduleMatmulForHVXPass.cpp:69-195),
  * which the reference runs as separate passes over HBM.
  */
-int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, int64_t M, int64_t N, int64_t K, int64_t ldx,
-                            int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
+int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                            int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
                             const float* rscale_in, void* stream);
 
 /* Wg[n,k] = fp16(W[n,k] * g[k]) (fp32 product, one rounding): the weight

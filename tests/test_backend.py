@@ -173,21 +173,65 @@ class OraclePkg(types.SimpleNamespace):
     def pack_gate_up(wg, wu):
         return torch.from_numpy(ref.pack_gate_up(wg.numpy(), wu.numpy()))
 
+    @staticmethod
+    def fold_rms_weight(w, g):
+        return (w.float() * g.float()[None, :]).half()
 
-def test_planner_matches_hot_path_patterns(backend):
+    @staticmethod
+    def rms_norm_linear(x, w, eps, epilogue=None, bias=None, rscale_out=None, rscale_in=None):
+        xn = ref.rms_norm(x.numpy(), np.ones(x.shape[-1], np.float32), eps)
+        if rscale_out is not None:
+            xf = x.float().numpy()
+            rscale_out.copy_(torch.from_numpy(1 / np.sqrt((xf * xf).mean(-1) + eps)))
+        if rscale_in is not None:  # the scales a previous call published
+            xn = x.float().numpy() * rscale_in.numpy()[:, None]
+        if epilogue == "silu_mul":
+            y = ref.gemm_epilogue(xn, w.numpy(), "nt", "silu_mul")
+        else:
+            y = ref.linear(xn, w.numpy(), None if bias is None else bias.numpy())
+        return torch.from_numpy(y).half()
+
+
+class QKVIn(nn.Module):
+    """Qwen2-style attention input: RMSNorm, then q/k/v projections with bias
+    (q and v consume the norm, k a second one without bias)."""
+
+    def __init__(self, h=64):
+        super().__init__()
+        self.norm = RMS(h)
+        self.norm2 = RMS(h)
+        self.q = nn.Linear(h, 64)
+        self.k = nn.Linear(h, 32, bias=False)
+        self.v = nn.Linear(h, 32)
+
+    def forward(self, x):
+        hs = self.norm(x)
+        return self.q(hs), self.v(hs), self.k(self.norm2(x))
+
+
+@pytest.fixture
+def oracle_kernels(monkeypatch):
+    from hexagon_mlir_amd.backend import graph
+
+    monkeypatch.setattr(graph, "_pkg", lambda: OraclePkg())
+
+
+def test_planner_matches_hot_path_patterns(backend, oracle_kernels):
     torch.manual_seed(0)
     model = Block().half()
     ep = backend.export_program(model, block_inputs())
     plan = backend.plan_program(ep, torch.device("cpu"), fusion=True)
     pats = sorted(p for p, _ in plan.kernels)
-    assert pats == ["attention", "attention", "linear", "linear_gelu", "rms_norm", "rms_norm", "silu_mul"], pats
+    # the norm feeding only gate/up is folded into that GEMM; F.rms_norm of
+    # the output stays a kernel
+    assert pats == ["attention", "attention", "linear", "linear_gelu", "rms_norm", "rms_silu_mul"], pats
     # nothing of the hot path is left to torch
     left = " ".join(plan.torch_ops)
     for op in ("linear", "matmul", "softmax", "rsqrt", "silu", "gelu", "rms_norm", "scaled_dot"):
         assert op not in left, left
 
 
-def test_planner_without_fusion_keeps_elementwise_ops(backend):
+def test_planner_without_fusion_keeps_elementwise_ops(backend, oracle_kernels):
     torch.manual_seed(0)
     plan = backend.plan_program(backend.export_program(Block().half(), block_inputs()), torch.device("cpu"),
                                 fusion=False)
@@ -196,13 +240,39 @@ def test_planner_without_fusion_keeps_elementwise_ops(backend):
     assert any("silu" in t for t in plan.torch_ops) and any("gelu" in t for t in plan.torch_ops)
 
 
-def test_planner_rewiring_is_numerically_right(backend, monkeypatch):
+def test_planner_folds_rmsnorm_into_projections(backend, oracle_kernels):
+    torch.manual_seed(0)
+    model = QKVIn().half()
+    x = torch.randn(6, 64, generator=torch.Generator().manual_seed(2)).half()
+    plan = backend.plan_program(backend.export_program(model, [x]), torch.device("cpu"), fusion=True)
+    assert sorted(p for p, _ in plan.kernels) == ["rms_linear"] * 3, plan.kernels
+    assert not any("rsqrt" in t or "linear" in t for t in plan.torch_ops), plan.torch_ops
+    got = plan.module(x)
+    exp = model.float()(x.float())
+    for g_, e in zip(got, exp):
+        assert ref.max_err_vs_scale(g_.float().numpy(), e.detach().numpy()) < 1e-2
+
+
+def test_planner_keeps_rmsnorm_with_other_users(backend, oracle_kernels):
+    class Two(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.norm = RMS(64)
+            self.q = nn.Linear(64, 32, bias=False)
+
+        def forward(self, x):
+            hs = self.norm(x)
+            return self.q(hs), hs * 2
+
+    plan = backend.plan_program(backend.export_program(Two().half(), [torch.randn(4, 64).half()]),
+                                torch.device("cpu"), fusion=True)
+    assert sorted(p for p, _ in plan.kernels) == ["linear", "rms_norm"]
+
+
+def test_planner_rewiring_is_numerically_right(backend, oracle_kernels):
     torch.manual_seed(0)
     model = Block().half()
     inputs = block_inputs(1)
-    from hexagon_mlir_amd.backend import graph
-
-    monkeypatch.setattr(graph, "_pkg", lambda: OraclePkg())
     plan = backend.plan_program(backend.export_program(model, inputs), torch.device("cpu"), fusion=True)
     got = plan.module(*inputs)
     exp = model.float()(*[t.float() for t in inputs])

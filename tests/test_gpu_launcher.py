@@ -8,7 +8,7 @@ import torch.nn as nn
 
 from gpu_util import TOL, normal, np32, uniform
 from oracle import hot_path as ref
-from test_backend import Block, block_inputs
+from test_backend import Block, QKVIn, block_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -64,7 +64,7 @@ def test_block_through_launcher(backend, dev, tmp_path):
     opts = backend.HexagonOptions(enableLWP=True).__dict__
     outs = launcher.run_torch_mlir(path, inputs, "block", str(tmp_path), iterations=2, options=opts)
     pats = sorted(p for p, _ in launcher.last_plan.kernels)
-    assert pats == ["attention", "attention", "linear", "linear_gelu", "rms_norm", "rms_norm", "silu_mul"]
+    assert pats == ["attention", "attention", "linear", "linear_gelu", "rms_norm", "rms_silu_mul"]
     exp = model.float()(*[t.float() for t in inputs])
     for o, e in zip(outs, exp):
         assert o.device.type == "cpu" and o.dtype == torch.float16
@@ -87,3 +87,19 @@ def test_fusion_off_gives_same_numbers(backend, dev, tmp_path):
                                                             options=backend.HexagonOptions(fusion=False).__dict__)
     for a, b in zip(on, off):
         assert ref.max_err_vs_scale(np32(a), np32(b)) <= TOL
+
+
+def test_rmsnorm_folded_into_qkv_on_gpu(backend, dev, tmp_path):
+    """Qwen2-style q/k/v with bias after an RMSNorm: three GEMMs, the first
+    takes the row statistics, no RMSNorm kernel; compared with the fp32 model."""
+    torch.manual_seed(0)
+    model = QKVIn(256).half()
+    x = torch.randn(77, 256, generator=torch.Generator().manual_seed(5)).half()
+    path = str(tmp_path / "qkv.pt2")
+    backend.write_program_to_file(backend.export_program(model, [x]), path)
+    launcher = backend.TorchMLIRHexagonLauncher()
+    outs = launcher.run_torch_mlir(path, [x], "qkv", str(tmp_path), iterations=2)
+    assert sorted(p for p, _ in launcher.last_plan.kernels) == ["rms_linear"] * 3
+    exp = model.float()(x.float())
+    for o, e in zip(outs, exp):
+        assert ref.max_err_vs_scale(np32(o), e.detach().numpy()) <= TOL

@@ -117,14 +117,14 @@ def test_rms_norm_linear_zero_row_and_scale_invariance(pkg, dev):
     assert torch.equal(y4[:7], y[:7])
 
 
-def test_rms_norm_linear_rejects_bias_epilogue(pkg, dev):
+def test_rms_norm_linear_rejects_gelu_epilogue(pkg, dev):
     lib = pkg.load_library()
     t = torch.zeros(64, 64, dtype=torch.float16, device=dev)
-    rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), 64, 64, 64, 64, 64, 64, 1,
+    rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), None, 64, 64, 64, 64, 64, 64, 3,
                                      ctypes.c_float(1e-5), None, None, None)
     assert rc == 1 and b"epilogue" in lib.hxmi_last_error()
     r = torch.zeros(64, dtype=torch.float32, device=dev)
-    rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), 64, 64, 64, 64, 64, 64, 0,
+    rc = lib.hxmi_rmsnorm_linear_f16(t.data_ptr(), t.data_ptr(), t.data_ptr(), None, 64, 64, 64, 64, 64, 64, 0,
                                      ctypes.c_float(1e-5), r.data_ptr(), r.data_ptr(), None)
     assert rc == 1 and b"exclusive" in lib.hxmi_last_error()
 
@@ -178,3 +178,26 @@ def test_rscale_in_second_consumer(pkg, dev, force_tile, tile, M, K):
     check(q, x, wqf.cpu(), ref.linear(xn, wq.numpy()), 1e-5)
     check(h, x, wguf.cpu(), ref.silu_mul_linear(xn, wg.numpy(), wu.numpy()), 1e-5, "silu_mul")
     assert ref.max_rel_err(np32(h), np32(h_rms)) <= 1e-3
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_rms_norm_linear_bias_every_tile(pkg, dev, force_tile, tile):
+    """Qwen2-style q/k/v: RMSNorm, then a projection with bias; the first
+    projection takes the statistics, the next reuses its row scales."""
+    force_tile(tile)
+    M, K = 200, 264
+    x = normal((M, K), 32)
+    g = _norm_weight(K, 33)
+    wq, wk = normal((128, K), 34, 0.05), normal((64, K), 35, 0.05)
+    bq, bk = normal((128,), 36, 0.5), normal((64,), 37, 0.5)
+    xd = x.to(dev)
+    wqf = pkg.fold_rms_weight(wq.to(dev), g.to(dev))
+    wkf = pkg.fold_rms_weight(wk.to(dev), g.to(dev))
+    rs = torch.empty(M, dtype=torch.float32, device=dev)
+    q = pkg.rms_norm_linear(xd, wqf, 1e-6, bias=bq.to(dev), rscale_out=rs).cpu()
+    k = pkg.rms_norm_linear(xd, wkf, 1e-6, bias=bk.to(dev), rscale_in=rs).cpu()
+    xn = ref.rms_norm_hf(x.numpy(), g.numpy(), 1e-6)
+    xn_exact = ref.rms_norm(x.numpy(), np.ones(K, np.float32), 1e-6)
+    for y, wf, w, b in ((q, wqf, wq, bq), (k, wkf, wk, bk)):
+        assert ref.max_rel_err(np32(y), ref.linear(xn_exact, np32(wf.cpu()), b.numpy())) <= TOL
+        assert ref.max_err_vs_scale(np32(y), ref.linear(xn, w.numpy(), b.numpy())) <= TOL
