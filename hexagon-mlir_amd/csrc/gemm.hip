@@ -207,11 +207,12 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 
 // Split K into slices when the output has too few tiles to occupy the 256
 // CUs and K is long enough that each slice still runs many K-steps.  Split
-// problems run 64x128 tiles (4 waves, up to three per CU); the slice count
-// aims at ~480 of them, each slice keeping >= 1024 of K.  Measured on the
-// TinyLlama down projection (512x2048x5632: 431 -> 464 TFLOP/s against
-// 128x128 tiles) and ViT-B/16 fc2 (1576x768x3072: 316 -> 376); with K below
-// 3072 (the 512-token QKV and O projections) every split measured slower.
+// problems run 64x128 tiles (4 waves, two per CU at three LDS stages).
+// Slices of >= 2048 of K that already give every CU a workgroup stop at
+// two; otherwise the slice count aims at ~480 workgroups, each slice keeping
+// >= 1024 of K (ViT-B/16 fc2, 1576x768x3072: 3 slices, 48.4 us per ViT
+// block against 52.7 with 2).  With K below 3072 (the 512-token QKV and O
+// projections) every split measured slower.
 // With int8 weights the slices run 64x64 tiles (Qwen2.5-0.5B down
 // projection at M = 256: 105 -> 128 TFLOP/s).
 int gemm_splits(const GemmProblem& p) {
@@ -219,6 +220,11 @@ int gemm_splits(const GemmProblem& p) {
   if (const char* e = getenv("HXMI_SPLITK")) return atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 127) / 128);
   if (tiles >= 384 || p.K < 3072) return 1;
+  // long slices: two of them once every CU has a workgroup (measured in the
+  // TinyLlama block sequence, weights not resident in L2: the 512x2048x5632
+  // down projection ran 80.9 us per block with 2 slices, 83.0 with 3, 83.3
+  // with 4, where each slice's fix-up traffic outweighs the extra workgroups)
+  if (p.dtype != DT_W8A16 && tiles * 2 >= 256 && p.K / 2 >= 2048) return 2;
   int s = (int)((480 + tiles / 2) / tiles);
   s = s < 1 ? 1 : (s > 4 ? 4 : s);
   while (s > 1 && p.K / s < 1024) --s;

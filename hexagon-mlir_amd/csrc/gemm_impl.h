@@ -570,19 +570,52 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       }
       __syncthreads();
       if (!is_last) return;
-      for (int sl = 0; sl < a.batch; ++sl) {
+      // GS slices' loads in flight at once (the small tiles, whose partial
+      // fragments fit in spare registers), then added in slice order
+      constexpr int GS = TN * TM == 1 ? 4 : (TN * TM == 2 ? 2 : 1);
+      if constexpr (GS == 1) {
+        for (int sl = 0; sl < a.batch; ++sl) {
 #pragma unroll
-        for (int i = 0; i < TN; ++i)
+          for (int i = 0; i < TN; ++i)
 #pragma unroll
-          for (int j = 0; j < TM; ++j)
+            for (int j = 0; j < TM; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const uint32_t off = (uint32_t)(sl * TILE_B + (((i * TM + j) * 4 + g) * NT + threadIdx.x) * 16);
-              const float4v v =
-                  __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rP, off, 0, kCoherent));
+              for (int g = 0; g < 4; ++g) {
+                const uint32_t off = (uint32_t)(sl * TILE_B + (((i * TM + j) * 4 + g) * NT + threadIdx.x) * 16);
+                const float4v v =
+                    __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rP, off, 0, kCoherent));
 #pragma unroll
-              for (int q = 0; q < 4; ++q) acc[i][j][4 * g + q] = sl == 0 ? v[q] : acc[i][j][4 * g + q] + v[q];
-            }
+                for (int q = 0; q < 4; ++q) acc[i][j][4 * g + q] = sl == 0 ? v[q] : acc[i][j][4 * g + q] + v[q];
+              }
+        }
+      } else for (int sl0 = 0; sl0 < a.batch; sl0 += GS) {
+        float4v part[GS][TN][TM][4];
+#pragma unroll
+        for (int u = 0; u < GS; ++u)
+#pragma unroll
+          for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                const int sl = sl0 + u;
+                const uint32_t off = (uint32_t)(sl * TILE_B + (((i * TM + j) * 4 + g) * NT + threadIdx.x) * 16);
+                part[u][i][j][g] = __builtin_bit_cast(
+                    float4v, __builtin_amdgcn_raw_buffer_load_b128(rP, sl < a.batch ? off : kOOB, 0, kCoherent));
+              }
+#pragma unroll
+        for (int u = 0; u < GS; ++u) {
+          if (sl0 + u >= a.batch) break;
+#pragma unroll
+          for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                  acc[i][j][4 * g + q] = sl0 + u == 0 ? part[u][i][j][g][q] : acc[i][j][4 * g + q] + part[u][i][j][g][q];
+        }
       }
     }
   }
