@@ -226,16 +226,26 @@ __global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
   const int tiles = (a.N + 15) / 16;
 
   // x fragments: fp16 step s covers k = 32 s + 8 kq + [0, 8); int8 step s
-  // covers k = 64 s + 16 kq + [0, 16) as fragments 2s and 2s + 1
-  const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
-  const bool mok = r16 < a.M;
-  const uint32_t xbase = (uint32_t)(r16 * a.ldx * 2);
+  // covers k = 64 s + 16 kq + [0, 16) as fragments 2s and 2s + 1.  The
+  // workgroup fetches them once into LDS (fragment f of lane l at
+  // (f * 64 + l) * 16, the 4 waves taking every 4th fragment), and every wave
+  // copies them to registers: one L2 read of x per workgroup, not per wave.
+  __shared__ __attribute__((aligned(16))) int4v xs[NX * 64];
+  {
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
+    const bool mok = r16 < a.M;
+    const uint32_t xbase = (uint32_t)(r16 * a.ldx * 2);
+#pragma unroll
+    for (int f0 = 0; f0 < NX; f0 += 4) {
+      const int f = f0 + w;
+      const int k = I8 ? (f / 2) * 64 + kq * 16 + (f & 1) * 8 : f * 32 + kq * 8;
+      xs[f * 64 + lane] = load16(rX, (mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
+    }
+  }
+  __syncthreads();
   int4v xv[NX];
 #pragma unroll
-  for (int f = 0; f < NX; ++f) {
-    const int k = I8 ? (f / 2) * 64 + kq * 16 + (f & 1) * 8 : f * 32 + kq * 8;
-    xv[f] = load16(rX, (mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
-  }
+  for (int f = 0; f < NX; ++f) xv[f] = xs[f * 64 + lane];
 
   for (int tile = blockIdx.x * 4 + w; tile < tiles; tile += gridDim.x * 4) {
     const int n0 = tile * 16;
