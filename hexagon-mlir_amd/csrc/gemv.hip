@@ -225,8 +225,8 @@ __global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
   const int nsteps = (a.K + KSTEP - 1) / KSTEP;
   const int tiles = (a.N + 15) / 16;
 
-  // x fragments: fp16 step s covers k = 32 s + 8 kq + [0, 8); int8 step s
-  // covers k = 64 s + 16 kq + [0, 16) as fragments 2s and 2s + 1.  The
+  // x fragments: fragment f covers k = 64 (f / 2) + 16 kq + 8 (f % 2) + [0, 8)
+  // (fp16 weight step f; int8 weight step s covers fragments 2s, 2s + 1).  The
   // workgroup fetches them once into LDS (fragment f of lane l at
   // (f * 64 + l) * 16, the 4 waves taking every 4th fragment), and every wave
   // copies them to registers: one L2 read of x per workgroup, not per wave.
@@ -238,14 +238,11 @@ __global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
 #pragma unroll
     for (int f0 = 0; f0 < NX; f0 += 4) {
       const int f = f0 + w;
-      const int k = I8 ? (f / 2) * 64 + kq * 16 + (f & 1) * 8 : f * 32 + kq * 8;
+      const int k = (f / 2) * 64 + kq * 16 + (f & 1) * 8;
       xs[f * 64 + lane] = load16(rX, (mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
     }
   }
   __syncthreads();
-  int4v xv[NX];
-#pragma unroll
-  for (int f = 0; f < NX; ++f) xv[f] = xs[f * 64 + lane];
 
   for (int tile = blockIdx.x * 4 + w; tile < tiles; tile += gridDim.x * 4) {
     const int n0 = tile * 16;
@@ -260,7 +257,11 @@ __global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int s = s0 + u;
-        const int k = s * KSTEP + kq * (KSTEP / 4);
+        // fp16: steps 2j and 2j+1 take the two 16-byte halves of the lane's
+        // 32 bytes at k = 64 j + 16 kq, so one instruction touches every
+        // 128-byte line of its 16 rows (the MFMA k order is free as long as
+        // x's fragments use the same one)
+        const int k = I8 ? s * KSTEP + kq * (KSTEP / 4) : (s / 2) * 64 + kq * 16 + (s & 1) * 8;
         wv[u] = load16(rW, (s < NS && rowok && k < a.K) ? wrow + (uint32_t)(k * esz) : kOOB);
       }
 #pragma unroll
@@ -268,12 +269,12 @@ __global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
         const int s = s0 + u;
         if (s < NS) {
           if constexpr (I8) {
-            acc = mfma16(dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]), __builtin_bit_cast(short8v, xv[2 * s]),
+            acc = mfma16(dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]), __builtin_bit_cast(short8v, xs[(2 * s) * 64 + lane]),
                          acc);
             acc = mfma16(dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]),
-                         __builtin_bit_cast(short8v, xv[2 * s + 1]), acc);
+                         __builtin_bit_cast(short8v, xs[(2 * s + 1) * 64 + lane]), acc);
           } else {
-            acc = mfma16(__builtin_bit_cast(short8v, wv[u]), __builtin_bit_cast(short8v, xv[s]), acc);
+            acc = mfma16(__builtin_bit_cast(short8v, wv[u]), __builtin_bit_cast(short8v, xs[s * 64 + lane]), acc);
           }
         }
       }
@@ -304,7 +305,7 @@ hipError_t launch_xreg(const VArgs& v, hipStream_t stream) {
   int cap = 512;  // two 4-wave workgroups per CU: each wave covers several tiles
   if (const char* e = getenv("HXMI_GEMV_XREG_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL((gemv_xreg<I8, 32, I8 ? 16 : 14>), dim3(blocks), dim3(256), 0, stream, v);
+  hipLaunchKernelGGL((gemv_xreg<I8, 32, I8 ? 16 : 32>), dim3(blocks), dim3(256), 0, stream, v);
   return hipGetLastError();
 }
 
