@@ -12,7 +12,7 @@ The directory name carries a dash, so it is imported under the module name
 ``hexagon_mlir_amd`` (see ``load_package`` in the repository's
 ``__graft_entry__.py``).
 """
-from . import hxmi
+from . import hxmi, weights
 from .hxmi import (
     HxmiError,
     HxmiNotBuiltError,
@@ -25,6 +25,7 @@ from .hxmi import (
     linear,
     load_library,
     pack_gate_up,
+    quantize_int8,
     rms_norm,
     rms_norm_linear,
     softmax,
@@ -33,6 +34,7 @@ from .hxmi import (
 
 __all__ = [
     "hxmi",
+    "weights",
     "HxmiError",
     "HxmiNotBuiltError",
     "attention",
@@ -44,6 +46,7 @@ __all__ = [
     "linear",
     "load_library",
     "pack_gate_up",
+    "quantize_int8",
     "rms_norm",
     "rms_norm_linear",
     "softmax",

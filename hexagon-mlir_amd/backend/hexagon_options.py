@@ -20,6 +20,10 @@ but have no GPU meaning; they affected Hexagon code generation only):
       "" = heuristic GEMM tile; "BM,BN" (e.g. "256,256") forces that tile.
   iterations
       Timing loop count of the Test_Info report (as the generated main()).
+  lowerConstantsInSeparateSharedObjects
+      The planned module's constants (weights after RMSNorm folding and
+      gate/up packing) are written to <func>.constants.safetensors in the
+      run's artifact folder and read back from there before the run.
   enableLWP
       Per-op timing (HIP events around every node) written to lwp.json in the
       run's artifact folder, the GPU analogue of the light-weight profiler.

@@ -67,6 +67,8 @@ class TorchMLIRHexagonLauncher(HexagonLauncherBase):
         if opts.tileSizes:
             os.environ["HXMI_GEMM_TILE"] = str(_tile_id(opts.tileSizes))
         plan = plan_program(program, self.device, fusion=opts.fusion)
+        if opts.lowerConstantsInSeparateSharedObjects:
+            self._constants_artifact(plan, local_dir, func_name)
         with open(os.path.join(local_dir, f"{func_name}.plan.txt"), "w") as f:
             f.write(plan.summary() + "\n")
         self.last_plan = plan
@@ -94,6 +96,26 @@ class TorchMLIRHexagonLauncher(HexagonLauncherBase):
         plan = self.compile_torch_mlir(local_dir, mlir_bytecode_path, func_name, options)
         print(f"Compilation from program file to GPU plan took {time.time() - start:.4f} seconds", flush=True)
         return self.execute_kernel(plan, inputs, func_name, local_dir, iterations, opts.enableLWP)
+
+    def _constants_artifact(self, plan: Plan, local_dir: str, func_name: str) -> str:
+        """The plan's constants (weights after folding and packing) written to
+        <func_name>.constants.safetensors, an artifact of their own as the
+        reference's split-constants mode produces
+        (triton_qcom_hexagon_backend_api.cc:196-214); the module's constants
+        are then overwritten with the values read back from that file, so the
+        run uses what the artifact holds."""
+        from safetensors.torch import load_file, save_file
+
+        path = os.path.join(local_dir, f"{func_name}.constants.safetensors")
+        named = dict(plan.module.named_parameters())
+        named.update(plan.module.named_buffers())
+        save_file({k: v.detach().to("cpu").clone().contiguous() for k, v in named.items()}, path,
+                  metadata={"format": "hxmi-constants", "func": func_name})
+        loaded = load_file(path, device=str(self.device))
+        with torch.no_grad():
+            for k, v in named.items():
+                v.copy_(loaded[k])
+        return path
 
     def execute_kernel(self, plan: Plan, inputs: list, func_name: str, local_dir: str, iterations: int = 1,
                        lwp: bool = False) -> list[Tensor]:

@@ -341,6 +341,19 @@ int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t
   return from_hip(hxmi::launch_fold_rms_weight(W, g, Wg, N, K, ldw, ldwg, (hipStream_t)stream), name);
 }
 
+int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, int64_t K, int64_t ldw, int64_t ldq,
+                                void* stream) {
+  const char* name = "hxmi_quantize_int8_rows_f16";
+  REQUIRE(N >= 0 && K >= 0, "%s: negative size", name);
+  if (N == 0 || K == 0) return ok();
+  REQUIRE(W && q && s, "%s: null pointer", name);
+  REQUIRE(ldw >= K && ldq >= K, "%s: leading dimension smaller than K", name);
+  REQUIRE(K % 8 == 0 && ldw % 8 == 0 && ldq % 8 == 0, "%s: K, ldw and ldq must be multiples of 8", name);
+  REQUIRE((uintptr_t)W % 16 == 0 && (uintptr_t)q % 8 == 0 && (uintptr_t)s % 2 == 0,
+          "%s: W must be 16-byte, q 8-byte aligned", name);
+  return from_hip(hxmi::launch_quantize_int8_rows(W, q, s, N, K, ldw, ldq, (hipStream_t)stream), name);
+}
+
 int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,
                             const hxmi_f16_t* inW) {
   const int rc = gemm_common(hxmi::DT_F16, inAct, inW, outM, nullptr, 1, n_row, n_col, n_inner, n_inner, n_col, n_col,

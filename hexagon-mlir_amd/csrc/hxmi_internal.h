@@ -52,6 +52,12 @@ struct GemmProblem {
 hipError_t launch_fold_rms_weight(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
                                   int64_t ldwg, hipStream_t stream);
 
+// s[n] = fp16 scale covering max_k |W[n][k]| / 127, q[n][k] = rint(W[n][k] / s[n]):
+// per-row symmetric int8 codes for the weight-only int8 path.  K, ldw, ldq
+// multiples of 8, W 16-byte and q 8-byte aligned (checked by the caller).
+hipError_t launch_quantize_int8_rows(const void* W, int8_t* q, void* s, int64_t N, int64_t K, int64_t ldw,
+                                     int64_t ldq, hipStream_t stream);
+
 // Split-K factor the dispatcher uses for p (1 = none) and the workspace bytes
 // it needs; both depend only on shapes and epilogue.
 int gemm_splits(const GemmProblem& p);

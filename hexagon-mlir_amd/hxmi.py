@@ -48,6 +48,7 @@ SIGNATURES = {
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
     "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_quantize_int8_rows_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
 }
 
@@ -270,6 +271,23 @@ def fold_rms_weight(w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
     _check(load_library().hxmi_fold_rmsnorm_weight_f16(w.data_ptr(), g.data_ptr(), out.data_ptr(), N, K, ldw, K,
                                                        _stream(w)))
     return out
+
+
+def quantize_int8(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel symmetric int8 codes of an fp16 weight [N, K]:
+    returns (q [N, K] int8, s [N] fp16) with s[n] the smallest fp16 step at or
+    above max|w[n]| / 127 and q = rint(w / s), so |w - q * s| <= s / 2; the
+    layout w8a16_linear takes.  K must be a multiple of 8."""
+    _require_gpu(w)
+    if w.dtype != torch.float16 or w.dim() != 2:
+        raise HxmiError("quantize_int8 takes a 2-D fp16 weight")
+    N, K = w.shape
+    ldw = _rowmajor(w, "w")
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty(N, dtype=torch.float16, device=w.device)
+    _check(load_library().hxmi_quantize_int8_rows_f16(w.data_ptr(), q.data_ptr(), s.data_ptr(), N, K, ldw, K,
+                                                      _stream(w)))
+    return q, s
 
 
 def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, epilogue: Optional[str] = None,

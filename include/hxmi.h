@@ -193,6 +193,22 @@ int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t
                                  int64_t ldwg, void* stream);
 
 /*
+ * Per-output-channel symmetric int8 quantisation, the weight layout
+ * hxmi_gemv_w8a16 reads:
+ *   s[n]   = fp16(max_k |W[n,k]| / 127), moved one fp16 step up if
+ *            127 * s[n] < max_k |W[n,k]| (so no code clips); 1 for a zero row
+ *   q[n,k] = rint(W[n,k] / s[n]) (round half to even), in [-127, 127]
+ * so |W[n,k] - q[n,k] * s[n]| <= s[n] / 2.  W [N,K] fp16 (ldw), q [N,K] int8
+ * (ldq), s [N] fp16; K, ldw and ldq multiples of 8, W 16-byte and q 8-byte
+ * aligned; W finite.
+ * Replaces: the int8 weights the reference can only take through MLIR's
+ * quant.qcast lowering (createLowerQuantOps, LinalgToLLVMPass.cpp:203-205);
+ * it has no weight quantiser of its own.
+ */
+int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, int64_t K, int64_t ldw, int64_t ldq,
+                                void* stream);
+
+/*
  * Fused attention, fp16: for each of bh (batch x head) slices,
  *   O[i] = softmax(scale * Q[i] . K^T) . V  over s_kv keys,
  * Q/O [s_q, d], K/V [s_kv, d] row-major (leading dims ld*, slice strides

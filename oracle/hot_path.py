@@ -24,6 +24,11 @@ Parity status per function (how each is pinned, see tests/test_oracle.py):
                               torch F.softmax
   w8a16_linear, dequant_int8  exact integer one-hot known answers, scale
                               linearity
+  quantize_int8_rows          exact known answers (w = integer * 2^-7),
+                              round-half-even ties vs Python's round(), the
+                              scale against a brute-force search over every
+                              fp16 value, sign symmetry and power-of-two
+                              equivariance
   sdpa                        composition of the above vs torch SDPA math
   vtcm_tile_sizes             the reference's lit expectation
                               (vtcm_tiling_static.mlir:80-88) and the
@@ -186,6 +191,24 @@ def sdpa(q, k, v, scale=None) -> np.ndarray:
 def dequant_int8(q) -> np.ndarray:
     """Integer weights as floats; exact for every int8 code."""
     return np.asarray(q).astype(np.int32).astype(F32)
+
+
+def quantize_int8_rows(w) -> tuple[np.ndarray, np.ndarray]:
+    """Per-output-channel symmetric int8 codes of fp16 weights [N, K]:
+    s[n] = the smallest fp16 value with 127 * s[n] >= max_k |w[n,k]| (fp16
+    round-to-nearest of max/127, one step up where that fell below; 1 for a
+    zero row), q = rint(w / s) (half to even).  The reference has no weight
+    quantiser (int8 enters only through MLIR's quant.qcast lowering,
+    lib/Conversion/LinalgToLLVM/LinalgToLLVMPass.cpp:203-205); this states
+    the rule the int8 path's loader uses."""
+    wf = np.asarray(w, dtype=np.float16).astype(F32)
+    amax = np.abs(wf).max(axis=1)
+    s = (amax / F32(127)).astype(np.float16)
+    low = s.astype(F32) * F32(127) < amax
+    s = np.where(low, np.nextafter(s, np.float16(np.inf)), s)
+    s = np.where(amax == 0, np.float16(1), s).astype(np.float16)
+    q = np.clip(np.rint(wf / s.astype(F32)[:, None]), -127, 127).astype(np.int8)
+    return q, s
 
 
 def w8a16_linear(x, q, s, bias=None) -> np.ndarray:

@@ -123,3 +123,20 @@ def test_workspace_queries(pkg):
     assert lib.hxmi_gemv_workspace_bytes(1, 151936, 896) == 0
     assert lib.hxmi_gemv_workspace_bytes(17, 896, 4864) == 0  # the GEMM's case
     assert lib.hxmi_w8a16_workspace_bytes(256, 896, 4864) > 0
+
+
+@pytest.mark.parametrize(
+    "args, msg",
+    [
+        ((16, 16, 16, -1, 8, 8, 8, None), "negative size"),
+        ((None, 16, 16, 4, 8, 8, 8, None), "null"),
+        ((16, 16, 16, 4, 12, 12, 12, None), "multiples of 8"),
+        ((16, 16, 16, 4, 16, 8, 16, None), "leading dimension"),
+        ((24, 16, 16, 4, 8, 8, 8, None), "aligned"),
+    ],
+)
+def test_quantizer_rejects_invalid_arguments(pkg, args, msg):
+    lib = pkg.load_library()
+    assert lib.hxmi_quantize_int8_rows_f16(*args) == 1
+    assert msg in lib.hxmi_last_error().decode()
+    assert lib.hxmi_quantize_int8_rows_f16(None, None, None, 0, 8, 8, 8, None) == 0

@@ -103,3 +103,30 @@ def test_rmsnorm_folded_into_qkv_on_gpu(backend, dev, tmp_path):
     exp = model.float()(x.float())
     for o, e in zip(outs, exp):
         assert ref.max_err_vs_scale(np32(o), e.detach().numpy()) <= TOL
+
+
+def test_constants_in_separate_artifact(backend, dev, tmp_path):
+    """lowerConstantsInSeparateSharedObjects: the folded / packed weights go
+    to <func>.constants.safetensors and the run reads them back from it; the
+    outputs are bit-identical to a run without the option."""
+    from safetensors import safe_open
+
+    torch.manual_seed(0)
+    model = QKVIn(256).half()
+    x = torch.randn(33, 256, generator=torch.Generator().manual_seed(6)).half()
+    path = str(tmp_path / "qkv.pt2")
+    backend.write_program_to_file(backend.export_program(model, [x]), path)
+    plain = backend.TorchMLIRHexagonLauncher().run_torch_mlir(path, [x], "plain", str(tmp_path))
+    launcher = backend.TorchMLIRHexagonLauncher()
+    opts = backend.HexagonOptions(lowerConstantsInSeparateSharedObjects=True).__dict__
+    split = launcher.run_torch_mlir(path, [x], "split", str(tmp_path), options=opts)
+    for a, b in zip(plain, split):
+        assert torch.equal(a, b)
+    folder = next(p for p in tmp_path.iterdir() if p.is_dir() and p.name.startswith("split-"))
+    art = folder / "split.constants.safetensors"
+    with safe_open(str(art), framework="pt") as f:
+        keys = set(f.keys())
+        assert f.metadata()["format"] == "hxmi-constants"
+    names = {k for k, _ in launcher.last_plan.module.named_buffers()}
+    names |= {k for k, _ in launcher.last_plan.module.named_parameters()}
+    assert keys == names and any("rmsfold" in k for k in keys)
