@@ -318,6 +318,43 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
             "sample": f"{n} passes of the full 512-token TinyLlama block (fp32 numpy oracle), {dt * 1e3:.1f} ms each"}
 
 
+def profile_suite(pkg, torch, dev, timer) -> None:
+    """Launches for counter runs: 4096^3 NT GEMM and the Qwen2.5-0.5B lm_head
+    GEMVs, each warmed up by time, then 5 launches (weights rotate over
+    copies so none is cache-resident), then five 256 MiB copies."""
+    g = torch.Generator().manual_seed(1)
+    a = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(dev)
+    b = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(dev)
+    c = torch.empty(4096, 4096, dtype=torch.float16, device=dev)
+    gemm = lambda i=0: pkg.gemm(a, b, b_layout="nt", out=c)
+    timer._warm(gemm)
+    for _ in range(5):
+        gemm()
+    H, V = 896, 151936
+    ws = [torch.empty(V, H, dtype=torch.float16, device=dev).normal_(0, 0.02) for _ in range(3)]
+    qs = [torch.randint(-127, 128, (V, H), dtype=torch.int8, device=dev) for _ in range(3)]
+    sc = (torch.rand(V, generator=g) * 9e-3 + 1e-3).half().to(dev)
+    for M in (1, 16):
+        x = torch.randn(M, H, generator=g).half().to(dev)
+        y = torch.empty(M, V, dtype=torch.float16, device=dev)
+        gemv = lambda i=0: pkg.gemv(x, ws[i % 3], out=y)
+        timer._warm(gemv)
+        for i in range(5):
+            gemv(i)
+    x = torch.randn(1, H, generator=g).half().to(dev)
+    y = torch.empty(1, V, dtype=torch.float16, device=dev)
+    w8 = lambda i=0: pkg.w8a16_linear(x, qs[i % 3], sc, out=y)
+    timer._warm(w8)
+    for i in range(5):
+        w8(i)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("[bench] profile suite: 4096^3 GEMM, lm_head GEMV fp16 M=1/16, int8 M=1, 5 x 256 MiB copies")
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed rocprof
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
@@ -342,6 +379,10 @@ def main() -> int:
     ap.add_argument("--profile", action="store_true",
                     help="for rocprofv3: run only the dominant kernel (gate/up SiLU-mul GEMM) --steps times, then a "
                          "256 MiB device copy 5 times (calibrates FETCH_SIZE/WRITE_SIZE), and exit")
+    ap.add_argument("--profile-suite", action="store_true",
+                    help="for rocprofv3 counter runs: the 4096^3 fp16 NT GEMM and the lm_head decode GEMVs (fp16 "
+                         "M=1 and M=16, int8 M=1), each warmed up and then launched 5 times, then the 256 MiB copy "
+                         "calibration, and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -357,6 +398,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     timer = Timer(torch)
 
+    if args.profile_suite:
+        profile_suite(pkg, torch, dev, timer)
+        return 0
     step, gate_up, block_tensors, _ = make_block(pkg, torch, dev)
     fl = tinyllama_flops()
     if args.profile:
