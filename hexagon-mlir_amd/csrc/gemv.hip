@@ -14,12 +14,11 @@
 //     fp32 sum once, after the K reduction;
 //   * partial sums of the KS waves are reduced through LDS.
 // The MFMA operand layout makes each wave instruction read 64 bytes of 16
-// rows, half cache lines.  For M <= 8 a second kernel (gemv_valu) uses the
-// vector ALUs instead: a lane load then covers 8 rows x 128 bytes (whole
-// lines), which lets the weights stream with the non-temporal policy.  For
-// M > 8 its x reads from LDS grow with M and bound it, so long weight
-// matrices with K <= 1024 (the lm_head) use a third kernel (gemv_xreg) that
-// holds x in registers and gives each wave whole 16-row tiles.
+// rows, half cache lines.  Two more kernels read whole lines (8 rows x 128
+// bytes per wave instruction, non-temporal), which HBM serves faster: for
+// long weight matrices with K <= 1024 (the lm_head, gate/up) gemv_pair still
+// multiplies on the MFMA units (each row read as two MFMA rows), and for
+// M <= 8 on other long matrices gemv_valu multiplies on the vector ALUs.
 #include <stdlib.h>
 
 #include <atomic>
@@ -208,104 +207,122 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
   }
 }
 
-// Short-K GEMV with x held in registers, for M <= 16 and K <= 32 * NX
-// (fp16; int8: K <= 32 * NX as well, two fragments per 64-k step).  Every
-// wave loads the B fragments of x for the whole K once, then streams whole
-// 16-row weight tiles: no K split, no LDS, no reduction, one MFMA chain per
-// tile.  Waves stride over the tiles (persistent), so x is loaded once per
-// wave however many tiles it covers.  Loads are issued U steps at a time.
-template <bool I8, int NX, int U>
-__global__ __launch_bounds__(256) void gemv_xreg(VArgs a) {
-  constexpr int KSTEP = I8 ? 64 : 32;  // k per weight load step
-  constexpr int NS = I8 ? NX / 2 : NX;  // max weight load steps per tile
+// Short-K GEMV on MFMA with whole-line weight loads, for M <= 16 and
+// K <= 1024.  A wave owns 8-row weight tiles and walks K in 128-byte windows
+// (fp16: 64 k, int8: 128 k); one wave load covers 8 rows x 128 contiguous
+// bytes (8 lanes per row), the row-streaming access pattern, which HBM
+// serves faster than the 16 rows x 64 bytes of the MFMA operand layout.
+// The MFMA 16x16x32 still takes the loaded registers as its A operand by
+// reading each weight row as two A rows: A row r' = 2 R + h holds half h of
+// row R's window (lane l: r' = l % 16, k group l / 16, 16-byte chunk
+// 4 h + l / 16 of the window).  One MFMA multiplies all 16 A rows by x's
+// first-half fragments, a second by its second-half fragments; the first
+// is right for the h = 0 rows, the second for h = 1, and a row's result is
+// the sum of its two valid halves.  That doubles the MFMA work, which
+// stays a few percent of the MFMA units at HBM speed.
+template <bool I8, int NWIN, int U>
+__global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
+  constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
+  constexpr int FPW = I8 ? 4 : 2;     // x fragments per window
+  constexpr int CK = KW / 8;          // k per 16-byte chunk
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r16 = lane & 15, kq = lane >> 4;
+  const int rp = lane & 15, kq = lane >> 4;
+  const int rr = rp >> 1, hh = rp & 1;
   const int esz = I8 ? 1 : 2;
-  const int nsteps = (a.K + KSTEP - 1) / KSTEP;
-  const int tiles = (a.N + 15) / 16;
+  const int nwin = (a.K + KW - 1) / KW;
+  const int tiles = (a.N + 7) / 8;
 
-  // x fragments: fragment f covers k = 64 (f / 2) + 16 kq + 8 (f % 2) + [0, 8)
-  // (fp16 weight step f; int8 weight step s covers fragments 2s, 2s + 1).  The
-  // workgroup fetches them once into LDS (fragment f of lane l at
-  // (f * 64 + l) * 16, the 4 waves taking every 4th fragment), and every wave
-  // copies them to registers: one L2 read of x per workgroup, not per wave.
-  __shared__ __attribute__((aligned(16))) int4v xs[NX * 64];
+  // x fragments, staged once per workgroup: window j, fragment q (half
+  // h = q / (FPW / 2), part p = q % (FPW / 2)) holds, for lane l, row l % 16
+  // of x at k = KW j + (KW / 2) h + CK (l / 16) + 8 p + [0, 8)
+  __shared__ __attribute__((aligned(16))) int4v xs[NWIN * FPW * 64];
   {
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
-    const bool mok = r16 < a.M;
-    const uint32_t xbase = (uint32_t)(r16 * a.ldx * 2);
+    const bool mok = rp < a.M;
+    const uint32_t xbase = (uint32_t)(rp * a.ldx * 2);
 #pragma unroll
-    for (int f0 = 0; f0 < NX; f0 += 4) {
+    for (int f0 = 0; f0 < NWIN * FPW; f0 += 4) {
       const int f = f0 + w;
-      const int k = (f / 2) * 64 + kq * 16 + (f & 1) * 8;
+      const int j = f / FPW, q = f % FPW;
+      const int k = KW * j + (KW / 2) * (q / (FPW / 2)) + CK * kq + 8 * (q % (FPW / 2));
       xs[f * 64 + lane] = load16(rX, (mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
     }
   }
   __syncthreads();
 
+  const int chunk = hh * 4 + kq;  // this lane's 16-byte chunk of every window
   for (int tile = blockIdx.x * 4 + w; tile < tiles; tile += gridDim.x * 4) {
-    const int n0 = tile * 16;
+    const int n0 = tile * 8;
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
-    const bool rowok = n0 + r16 < a.N;
-    const uint32_t wrow = (uint32_t)(r16 * a.ldw * esz);
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    const bool rowok = n0 + rr < a.N;
+    const uint32_t wrow = (uint32_t)(rr * a.ldw * esz + chunk * 16);
+    float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s0 = 0; s0 < NS; s0 += U) {
-      if (s0 >= nsteps) break;
+    for (int j0 = 0; j0 < NWIN; j0 += U) {
+      if (j0 >= nwin) break;
       int4v wv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int s = s0 + u;
-        // fp16: steps 2j and 2j+1 take the two 16-byte halves of the lane's
-        // 32 bytes at k = 64 j + 16 kq, so one instruction touches every
-        // 128-byte line of its 16 rows (the MFMA k order is free as long as
-        // x's fragments use the same one)
-        const int k = I8 ? s * KSTEP + kq * (KSTEP / 4) : (s / 2) * 64 + kq * 16 + (s & 1) * 8;
-        wv[u] = load16(rW, (s < NS && rowok && k < a.K) ? wrow + (uint32_t)(k * esz) : kOOB);
+        const int j = j0 + u;
+        const bool ok = j < NWIN && rowok && (KW * j + CK * chunk) < a.K;
+        wv[u] = load16_nt(rW, ok ? wrow + (uint32_t)(j * 128) : kOOB);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int s = s0 + u;
-        if (s < NS) {
+        const int j = j0 + u;
+        if (j < NWIN) {
           if constexpr (I8) {
-            acc = mfma16(dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]), __builtin_bit_cast(short8v, xs[(2 * s) * 64 + lane]),
-                         acc);
-            acc = mfma16(dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]),
-                         __builtin_bit_cast(short8v, xs[(2 * s + 1) * 64 + lane]), acc);
+            const short8v lo = dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
+            const short8v hi = dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
+            acc0 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
+            acc0 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
+            acc1 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
+            acc1 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
           } else {
-            acc = mfma16(__builtin_bit_cast(short8v, wv[u]), __builtin_bit_cast(short8v, xs[s * 64 + lane]), acc);
+            const short8v wf = __builtin_bit_cast(short8v, wv[u]);
+            acc0 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
+            acc1 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
           }
         }
       }
     }
-    // D[n][m]: lane holds m = lane % 16, n = 4*(lane / 16) + 0..3
+    // D[r'][m]: lane holds m = lane % 16 and A rows r' = 4 (lane / 16) + i,
+    // i.e. halves 0, 1 of weight row n0 + 2 (lane / 16) and of the next row
     const int m = lane & 15;
-    const int n = n0 + 4 * (lane >> 4);
-    if (m < a.M && n < a.N) {
-      float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-      if (I8) {
+    const int n = n0 + 2 * kq;
+    if (m < a.M) {
+      float v[2] = {acc0[0] + acc1[1], acc0[2] + acc1[3]};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] *= (float)((const _Float16*)a.scale)[n + q];
+      for (int q = 0; q < 2; ++q) {
+        if (n + q < a.N) {
+          if (I8) v[q] *= (float)((const _Float16*)a.scale)[n + q];
+          if (a.bias) v[q] += (float)((const _Float16*)a.bias)[n + q];
+        }
       }
-      if (a.bias) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] += (float)((const _Float16*)a.bias)[n + q];
+      _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+      if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
+        _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+        *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
+      } else {
+        if (n < a.N) yrow[0] = (_Float16)v[0];
+        if (n + 1 < a.N) yrow[1] = (_Float16)v[1];
       }
-      _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-      *(short4v*)(a.y + ((int64_t)m * a.ldy + n) * 2) = __builtin_bit_cast(short4v, h);
     }
   }
 }
 
 template <bool I8>
-hipError_t launch_xreg(const VArgs& v, hipStream_t stream) {
-  const int tiles = (v.N + 15) / 16;
+hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
+  const int tiles = (v.N + 7) / 8;
   int blocks = (tiles + 3) / 4;
-  int cap = 512;  // two 4-wave workgroups per CU: each wave covers several tiles
-  if (const char* e = getenv("HXMI_GEMV_XREG_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
+  // four workgroups per CU (32 KB of staged x each), waves striding over
+  // the tiles: measured on the 896 -> 151936 lm_head, 512 / 768 / 1024 /
+  // 1280 / 2048 workgroups gave 49.3 / 47.7 / 46.5 / 55.4 / 48.5 us at M = 16
+  int cap = 1024;
+  if (const char* e = getenv("HXMI_GEMV_PAIR_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL((gemv_xreg<I8, 32, I8 ? 16 : 32>), dim3(blocks), dim3(256), 0, stream, v);
+  hipLaunchKernelGGL((gemv_pair<I8, I8 ? 8 : 16, I8 ? 8 : 16>), dim3(blocks), dim3(256), 0, stream, v);
   return hipGetLastError();
 }
 
@@ -475,7 +492,7 @@ hipError_t launch_sel(int tpb, int ks, const VArgs& v, hipStream_t stream) {
 // K groups across workgroups (kg).
 struct GemvPlan {
   int tpb = 1, ks = 8, kg = 1;
-  bool valu = false, xreg = false;
+  bool valu = false, pair = false;
 };
 
 static GemvPlan gemv_plan(const GemvProblem& p) {
@@ -494,23 +511,30 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   // tuning overrides (launch shape only; every shape computes the same sums)
   if (const char* e = getenv("HXMI_GEMV_TPB")) g.tpb = atoi(e) == 4 ? 4 : (atoi(e) == 2 ? 2 : 1);
   if (const char* e = getenv("HXMI_GEMV_KS")) g.ks = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : 4);
-  // vector-ALU row streaming: small M, x fits the LDS, enough row groups
-  // (measured on the Qwen2.5-0.5B shapes: the row-streaming kernel wins for
-  // long weight matrices -- lm_head -- up to M = 8 (int8: 4) and for M = 1
-  // from N = 4096; the MFMA tiles win where K must be split across waves)
+  // Measured on the Qwen2.5-0.5B shapes (graph replays, weights rotating
+  // past the Infinity Cache):
+  //  * whole-line MFMA kernel (K <= 1024): long weight matrices -- lm_head
+  //    M = 16 54.8 -> 46.3 us and M = 4 44.0 -> 41.2 us against the other
+  //    two, gate/up 896 -> 9728 at M = 16 8.3 -> 7.0 us; even at fp16
+  //    M = 1; behind row streaming for int8 at M <= 4 (lm_head 25.9 vs
+  //    22.6 us) and behind the 16-row MFMA tiles below N ~ 8192 (too few
+  //    8-row tiles to fill the GPU);
+  //  * vector-ALU row streaming: M = 1 from N = 4096, int8 M <= 4 from
+  //    N = 32768, and fp16 M <= 8 on long matrices whose K is too long for
+  //    the whole-line kernel;
+  //  * the 16-row MFMA tiles elsewhere (K split across waves).
   const int kstep_v = p.w_int8 ? 128 : 64;
   const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
   const bool fits = p.M <= 16 && p.M * kpad * 2 <= 64 * 1024;
-  g.valu = fits && p.M <= 8 && (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
-  // x in registers (K <= 1024): long weight matrices that the row-streaming
-  // kernel does not take
   const bool xfits = p.K <= 1024;
-  g.xreg = !g.valu && xfits && tiles16 >= 2048;
+  g.pair = xfits && p.N >= 8192 && (!p.w_int8 || p.M > 4);
+  g.valu = !g.pair && fits && p.M <= 8 &&
+           (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
   if (const char* e = getenv("HXMI_GEMV_PATH")) {
     g.valu = (e[0] == 'v') && fits;
-    g.xreg = (e[0] == 'x') && xfits;
+    g.pair = (e[0] == 'p') && xfits;
   }
-  if (g.valu || g.xreg) return g;
+  if (g.valu || g.pair) return g;
   // few row groups, each streaming a long K (e.g. a down projection
   // 4864 -> 896): split K over 2-4 workgroups per row group.  Combining the
   // partial tiles costs ~2 us of round trips to memory, so (measured on the
@@ -531,7 +555,7 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
 
 int64_t gemv_workspace_bytes(const GemvProblem& p) {
   const GemvPlan g = gemv_plan(p);
-  if (g.valu || g.xreg || g.kg <= 1) return 0;
+  if (g.valu || g.pair || g.kg <= 1) return 0;
   const int64_t tiles = (p.N + g.tpb * 16 - 1) / (g.tpb * 16) * g.tpb;  // 16-row tiles of whole row groups
   return gemv_counter_bytes(tiles) + tiles * g.kg * 1024;
 }
@@ -555,7 +579,7 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.epoch = 0;
   const GemvPlan g = gemv_plan(p);
   if (g.valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
-  if (g.xreg) return p.w_int8 ? launch_xreg<true>(v, stream) : launch_xreg<false>(v, stream);
+  if (g.pair) return p.w_int8 ? launch_pair<true>(v, stream) : launch_pair<false>(v, stream);
   if (g.kg > 1 && p.ws && p.ws_bytes >= gemv_workspace_bytes(p) && ((uintptr_t)p.ws % 256) == 0) {
     static std::atomic<unsigned long long> calls{1};
     v.kg = g.kg;

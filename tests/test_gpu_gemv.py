@@ -69,7 +69,8 @@ def test_w8a16_qwen_shapes(pkg, dev, M, K, N):
 @pytest.fixture
 def gemv_path(monkeypatch):
     """Force the decode kernel: "mfma" (16-row MFMA tiles, K split over
-    waves), "valu" (row streaming) or "xreg" (x in registers, K <= 1024)."""
+    waves), "valu" (row streaming) or "pair" (8-row tiles, whole-line
+    loads, each row read as two MFMA rows, K <= 1024)."""
 
     def force(path):
         monkeypatch.setenv("HXMI_GEMV_PATH", path)
@@ -77,7 +78,7 @@ def gemv_path(monkeypatch):
     return force
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu", "xreg"])
+@pytest.mark.parametrize("path", ["mfma", "valu", "pair"])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("N,K", [(4100, 904), (1028, 136), (8, 64)])
 def test_gemv_both_paths(pkg, dev, gemv_path, path, M, N, K):
@@ -90,7 +91,7 @@ def test_gemv_both_paths(pkg, dev, gemv_path, path, M, N, K):
     assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu", "xreg"])
+@pytest.mark.parametrize("path", ["mfma", "valu", "pair"])
 @pytest.mark.parametrize("M", [1, 3, 8])
 @pytest.mark.parametrize("N,K", [(4104, 912), (264, 144)])
 def test_w8a16_both_paths(pkg, dev, gemv_path, path, M, N, K):
@@ -103,7 +104,7 @@ def test_w8a16_both_paths(pkg, dev, gemv_path, path, M, N, K):
     assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu", "xreg"])
+@pytest.mark.parametrize("path", ["mfma", "valu", "pair"])
 def test_w8a16_onehot_exact_both_paths(pkg, dev, gemv_path, path):
     gemv_path(path)
     d = np.load(GOLDEN / "w8_onehot.npz")
@@ -263,11 +264,12 @@ def test_gemv_k_groups_graph_replays(pkg, dev):
 
 
 @pytest.mark.parametrize("M", [1, 7, 16])
-@pytest.mark.parametrize("N,K", [(2056, 1024), (40, 8), (300, 520), (33000, 896)])
-def test_gemv_xreg(pkg, dev, gemv_path, M, N, K):
-    # x held in registers for the whole K: K up to 1024, ragged K steps and
-    # row tiles, more tiles than waves (each wave strides over several)
-    gemv_path("xreg")
+@pytest.mark.parametrize("N,K", [(2056, 1024), (40, 8), (300, 520), (33000, 896), (1004, 72), (151936, 896)])
+def test_gemv_pair(pkg, dev, gemv_path, M, N, K):
+    # x staged for the whole K: K up to 1024, ragged 128-byte windows and
+    # 8-row tiles, more tiles than waves (each wave strides over several),
+    # the lm_head shape
+    gemv_path("pair")
     x = normal((M, K), 71 + M)
     w = normal((N, K), 72, 0.05)
     b = normal((N,), 73)
@@ -277,9 +279,9 @@ def test_gemv_xreg(pkg, dev, gemv_path, M, N, K):
 
 
 @pytest.mark.parametrize("M", [1, 16])
-@pytest.mark.parametrize("N,K", [(2056, 1024), (24, 16), (33000, 896)])
-def test_w8a16_xreg(pkg, dev, gemv_path, M, N, K):
-    gemv_path("xreg")
+@pytest.mark.parametrize("N,K", [(2056, 1024), (24, 16), (33000, 896), (1000, 144)])
+def test_w8a16_pair(pkg, dev, gemv_path, M, N, K):
+    gemv_path("pair")
     x = normal((M, K), 81 + M)
     q, s = int8_weights(N, K, 82)
     b = normal((N,), 83)
