@@ -45,6 +45,8 @@ struct VArgs {
   unsigned long long epoch;
 };
 
+typedef float float2v __attribute__((ext_vector_type(2)));
+
 __host__ __device__ constexpr int64_t gemv_counter_bytes(int64_t tiles) { return (tiles * 8 + 255) / 256 * 256; }
 
 __device__ __forceinline__ float4v mfma16(short8v a, short8v b, float4v c) {
@@ -312,6 +314,107 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   }
 }
 
+// Long-K GEMV (K > 1024, few rows: down projections) with the same
+// whole-line loads and row pairing: one workgroup per 8-row tile, its KS
+// waves splitting K into contiguous runs of 128-byte windows, partial sums
+// reduced through LDS.  Each wave loads its own x fragments (x is a few KB
+// and stays in L2), so a tile costs one memory round trip plus the
+// reduction, with no cross-workgroup fix-up.
+template <bool I8, int KS, int U>
+__global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
+  constexpr int KW = I8 ? 128 : 64;
+  constexpr int FPW = I8 ? 4 : 2;
+  constexpr int CK = KW / 8;
+  __shared__ float2v red[KS][64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rp = lane & 15, kq = lane >> 4;
+  const int rr = rp >> 1, hh = rp & 1;
+  const int chunk = hh * 4 + kq;
+  const int esz = I8 ? 1 : 2;
+  const int n0 = blockIdx.x * 8;
+  const int nwin = (a.K + KW - 1) / KW;
+  const int per = (nwin + KS - 1) / KS;
+  const int j_begin = min(nwin, w * per), j_end = min(nwin, j_begin + per);
+
+  const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
+  const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
+  const bool rowok = n0 + rr < a.N;
+  const uint32_t wrow = (uint32_t)(rr * a.ldw * esz + chunk * 16);
+  const bool mok = rp < a.M;
+  const uint32_t xbase = (uint32_t)(rp * a.ldx * 2);
+
+  float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = j_begin; j0 < j_end; j0 += U) {
+    int4v wv[U], xv[U][FPW];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + u;
+      const bool jok = j < j_end;
+      wv[u] = load16_nt(rW, (jok && rowok && (KW * j + CK * chunk) < a.K) ? wrow + (uint32_t)(j * 128) : kOOB);
+#pragma unroll
+      for (int q = 0; q < FPW; ++q) {
+        const int k = KW * j + (KW / 2) * (q / (FPW / 2)) + CK * kq + 8 * (q % (FPW / 2));
+        xv[u][q] = load16(rX, (jok && mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u < j_end) {
+        if constexpr (I8) {
+          const short8v lo = dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
+          const short8v hi = dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
+          acc0 = mfma16(lo, __builtin_bit_cast(short8v, xv[u][0]), acc0);
+          acc0 = mfma16(hi, __builtin_bit_cast(short8v, xv[u][1]), acc0);
+          acc1 = mfma16(lo, __builtin_bit_cast(short8v, xv[u][2]), acc1);
+          acc1 = mfma16(hi, __builtin_bit_cast(short8v, xv[u][3]), acc1);
+        } else {
+          const short8v wf = __builtin_bit_cast(short8v, wv[u]);
+          acc0 = mfma16(wf, __builtin_bit_cast(short8v, xv[u][0]), acc0);
+          acc1 = mfma16(wf, __builtin_bit_cast(short8v, xv[u][1]), acc1);
+        }
+      }
+    }
+  }
+  // lane: column m = lane % 16 of weight rows n0 + 2 (lane / 16) + {0, 1}
+  red[w][lane] = float2v{acc0[0] + acc1[1], acc0[2] + acc1[3]};
+  __syncthreads();
+  if (w != 0) return;
+  float2v s = red[0][lane];
+#pragma unroll
+  for (int q = 1; q < KS; ++q) s += red[q][lane];
+  const int m = lane & 15;
+  const int n = n0 + 2 * kq;
+  if (m < a.M) {
+    float v[2] = {s[0], s[1]};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (n + q < a.N) {
+        if (I8) v[q] *= (float)((const _Float16*)a.scale)[n + q];
+        if (a.bias) v[q] += (float)((const _Float16*)a.bias)[n + q];
+      }
+    }
+    _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+    if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
+      _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+      *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
+    } else {
+      if (n < a.N) yrow[0] = (_Float16)v[0];
+      if (n + 1 < a.N) yrow[1] = (_Float16)v[1];
+    }
+  }
+}
+
+template <bool I8>
+hipError_t launch_pair_ks(const VArgs& v, int ks, hipStream_t stream) {
+  const int blocks = (v.N + 7) / 8;
+  if (ks >= 16)
+    hipLaunchKernelGGL((gemv_pair_ks<I8, 16, I8 ? 4 : 8>), dim3(blocks), dim3(1024), 0, stream, v);
+  else
+    hipLaunchKernelGGL((gemv_pair_ks<I8, 8, I8 ? 4 : 8>), dim3(blocks), dim3(512), 0, stream, v);
+  return hipGetLastError();
+}
+
 template <bool I8>
 hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   const int tiles = (v.N + 7) / 8;
@@ -492,7 +595,7 @@ hipError_t launch_sel(int tpb, int ks, const VArgs& v, hipStream_t stream) {
 // K groups across workgroups (kg).
 struct GemvPlan {
   int tpb = 1, ks = 8, kg = 1;
-  bool valu = false, pair = false;
+  bool valu = false, pair = false, pair_ks = false;
 };
 
 static GemvPlan gemv_plan(const GemvProblem& p) {
@@ -522,19 +625,33 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   //  * vector-ALU row streaming: M = 1 from N = 4096, int8 M <= 4 from
   //    N = 32768, and fp16 M <= 8 on long matrices whose K is too long for
   //    the whole-line kernel;
+  //  * whole-line kernel with K split over a workgroup's waves: K > 1024
+  //    on at most 2048 rows (down projections; one workgroup per 8-row
+  //    tile, so at most 256 workgroups): 4864 -> 896 at M = 1 8.1 -> 5.7 us,
+  //    5632 -> 2048 9.6 -> 6.7 us, 2048 -> 896 at M = 16 6.3 -> 4.9 us; 16
+  //    waves only where each still gets >= 4 windows (M > 4: 4864 -> 896 at
+  //    M = 16 8.7 -> 8.5 us); behind the 16-row tiles from N = 2560;
   //  * the 16-row MFMA tiles elsewhere (K split across waves).
   const int kstep_v = p.w_int8 ? 128 : 64;
   const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
   const bool fits = p.M <= 16 && p.M * kpad * 2 <= 64 * 1024;
   const bool xfits = p.K <= 1024;
   g.pair = xfits && p.N >= 8192 && (!p.w_int8 || p.M > 4);
-  g.valu = !g.pair && fits && p.M <= 8 &&
+  g.pair_ks = !xfits && p.N <= 2048;
+  if (g.pair_ks) {
+    const int64_t nwin = (p.K + (p.w_int8 ? 127 : 63)) / (p.w_int8 ? 128 : 64);
+    g.ks = (p.M > 4 && nwin >= 64) ? 16 : 8;
+    if (const char* e = getenv("HXMI_GEMV_KS")) g.ks = atoi(e) >= 16 ? 16 : 8;
+  }
+  g.valu = !g.pair && !g.pair_ks && fits && p.M <= 8 &&
            (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
   if (const char* e = getenv("HXMI_GEMV_PATH")) {
     g.valu = (e[0] == 'v') && fits;
     g.pair = (e[0] == 'p') && xfits;
+    g.pair_ks = (e[0] == 'k');
+    if (g.pair_ks && !getenv("HXMI_GEMV_KS")) g.ks = 8;
   }
-  if (g.valu || g.pair) return g;
+  if (g.valu || g.pair || g.pair_ks) return g;
   // few row groups, each streaming a long K (e.g. a down projection
   // 4864 -> 896): split K over 2-4 workgroups per row group.  Combining the
   // partial tiles costs ~2 us of round trips to memory, so (measured on the
@@ -555,7 +672,7 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
 
 int64_t gemv_workspace_bytes(const GemvProblem& p) {
   const GemvPlan g = gemv_plan(p);
-  if (g.valu || g.pair || g.kg <= 1) return 0;
+  if (g.valu || g.pair || g.pair_ks || g.kg <= 1) return 0;
   const int64_t tiles = (p.N + g.tpb * 16 - 1) / (g.tpb * 16) * g.tpb;  // 16-row tiles of whole row groups
   return gemv_counter_bytes(tiles) + tiles * g.kg * 1024;
 }
@@ -580,6 +697,7 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   const GemvPlan g = gemv_plan(p);
   if (g.valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
   if (g.pair) return p.w_int8 ? launch_pair<true>(v, stream) : launch_pair<false>(v, stream);
+  if (g.pair_ks) return p.w_int8 ? launch_pair_ks<true>(v, g.ks, stream) : launch_pair_ks<false>(v, g.ks, stream);
   if (g.kg > 1 && p.ws && p.ws_bytes >= gemv_workspace_bytes(p) && ((uintptr_t)p.ws % 256) == 0) {
     static std::atomic<unsigned long long> calls{1};
     v.kg = g.kg;

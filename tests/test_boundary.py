@@ -115,10 +115,13 @@ def test_workspace_queries(pkg):
     # 4096^3 fills the GPU without splitting; batched / short-K never split
     assert lib.hxmi_gemm_workspace_bytes(4096, 4096, 4096, 1, 0) == 0
     assert lib.hxmi_gemm_workspace_bytes(512, 2048, 512, 1, 0) == 0
-    # decode GEMV: a down projection (few rows, long K) splits K over
-    # workgroups; wide outputs and the lm_head never do
-    assert lib.hxmi_w8a16_workspace_bytes(16, 896, 4864) > 0
-    assert lib.hxmi_gemv_workspace_bytes(1, 896, 4864) > 0
+    # decode GEMV: long K on 2560 rows splits K over workgroups; down
+    # projections (<= 2048 rows) split K inside one workgroup per row tile,
+    # wide outputs and the lm_head never split
+    assert lib.hxmi_w8a16_workspace_bytes(16, 2560, 8192) > 0
+    assert lib.hxmi_gemv_workspace_bytes(1, 2560, 8192) > 0
+    assert lib.hxmi_gemv_workspace_bytes(1, 896, 4864) == 0
+    assert lib.hxmi_w8a16_workspace_bytes(16, 896, 4864) == 0
     assert lib.hxmi_gemv_workspace_bytes(1, 4864, 896) == 0
     assert lib.hxmi_gemv_workspace_bytes(1, 151936, 896) == 0
     assert lib.hxmi_gemv_workspace_bytes(17, 896, 4864) == 0  # the GEMM's case

@@ -207,21 +207,22 @@ def test_w8a16_onehot_exact_k_groups(pkg, dev, gemv_kgroups):
     assert np.array_equal(y.cpu().numpy().astype(np.int32), d["y"][rows])
 
 
-def test_gemv_down_projection_splits_by_default(pkg, dev):
-    """The Qwen2.5-0.5B down projection (4864 -> 896) splits K by default; the
-    result is deterministic (partials are added in K-group order) and one
-    workspace serves calls of different shapes back to back."""
+def test_gemv_long_k_splits_by_default(pkg, dev):
+    """A long-K GEMV on 2560 rows (8192 -> 2560) splits K over workgroups by
+    default; the result is deterministic (partials are added in K-group
+    order) and one workspace serves calls of different shapes back to back."""
     lib = pkg.load_library()
-    assert lib.hxmi_gemv_workspace_bytes(1, 896, 4864) > 0
+    N, K = 2560, 8192
+    assert lib.hxmi_gemv_workspace_bytes(1, N, K) > 0
     assert lib.hxmi_gemv_workspace_bytes(1, 4864, 896) == 0
-    nbytes = max(lib.hxmi_gemv_workspace_bytes(m, 896, 4864) for m in (1, 16))
+    nbytes = max(lib.hxmi_gemv_workspace_bytes(m, N, K) for m in (1, 16))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    w = normal((896, 4864), 51, 0.05).to(dev)
+    w = normal((N, K), 51, 0.05).to(dev)
     outs = []
     for M in (1, 16, 1, 16, 1):
-        x = normal((M, 4864), 52 + M).to(dev)
-        y = torch.empty((M, 896), dtype=torch.float16, device=dev)
-        rc = lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, 896, 4864, 4864, 4864, 896,
+        x = normal((M, K), 52 + M).to(dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        rc = lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, N, K, K, K, N,
                                ws.data_ptr(), nbytes, None)
         assert rc == 0, lib.hxmi_last_error()
         outs.append(y.cpu())
@@ -232,7 +233,7 @@ def test_gemv_down_projection_splits_by_default(pkg, dev):
 def test_gemv_k_groups_graph_replays(pkg, dev):
     """Captured split-K GEMV: the arrival counters reset themselves, so every
     replay (with eager calls on the same workspace between them) matches."""
-    M, N, K = 1, 896, 4864
+    M, N, K = 1, 2560, 8192
     lib = pkg.load_library()
     nbytes = lib.hxmi_gemv_workspace_bytes(M, N, K)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -300,3 +301,46 @@ def test_gemv_valu_two_row_blocks(pkg, dev, gemv_path, M, N, K):
     y = pkg.gemv(x.to(dev), w.to(dev))
     torch.cuda.synchronize()
     assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("ks", ["8", "16"])
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("N,K", [(896, 4864), (2048, 5632), (1004, 2056), (40, 8), (300, 1288)])
+def test_gemv_pair_ksplit(pkg, dev, gemv_path, monkeypatch, ks, M, N, K):
+    # whole-line loads with K split over the workgroup's waves: down
+    # projections, ragged windows and 8-row tiles, waves left without K
+    gemv_path("ksplit")
+    monkeypatch.setenv("HXMI_GEMV_KS", ks)
+    x = normal((M, K), 91 + M)
+    w = normal((N, K), 92, 0.05)
+    b = normal((N,), 93)
+    y = pkg.gemv(x.to(dev), w.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("ks", ["8", "16"])
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("N,K", [(896, 4864), (1000, 2064), (24, 16)])
+def test_w8a16_pair_ksplit(pkg, dev, gemv_path, monkeypatch, ks, M, N, K):
+    gemv_path("ksplit")
+    monkeypatch.setenv("HXMI_GEMV_KS", ks)
+    x = normal((M, K), 95 + M)
+    q, s = int8_weights(N, K, 96)
+    b = normal((N,), 97)
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
+
+
+def test_w8a16_onehot_exact_pair_ksplit(pkg, dev, gemv_path):
+    gemv_path("ksplit")
+    d = np.load(GOLDEN / "w8_onehot.npz")
+    q, cols = torch.from_numpy(d["q"]), d["cols"]
+    M = 5
+    rows = np.resize(np.arange(len(cols)), M)
+    x = torch.zeros((M, q.shape[1]), dtype=torch.float16)
+    x[np.arange(M), cols[rows]] = 1
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), torch.ones(q.shape[0], dtype=torch.float16, device=dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().astype(np.int32), d["y"][rows])
