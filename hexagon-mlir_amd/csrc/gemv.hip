@@ -14,11 +14,13 @@
 //     fp32 sum once, after the K reduction;
 //   * partial sums of the KS waves are reduced through LDS.
 // The MFMA operand layout makes each wave instruction read 64 bytes of 16
-// rows, half cache lines.  Two more kernels read whole lines (8 rows x 128
-// bytes per wave instruction, non-temporal), which HBM serves faster: for
-// long weight matrices with K <= 1024 (the lm_head, gate/up) gemv_pair still
-// multiplies on the MFMA units (each row read as two MFMA rows), and for
-// M <= 8 on other long matrices gemv_valu multiplies on the vector ALUs.
+// rows, half cache lines.  Three more kernels read whole lines (8 rows x 128
+// bytes per wave instruction, non-temporal), which HBM serves faster:
+//   * gemv_pair: long weight matrices with K <= 1024 (the lm_head, gate/up),
+//     still on the MFMA units (each row read as two MFMA rows);
+//   * gemv_pair_ks: K > 1024 on at most 2048 rows (down projections), the
+//     same loads with K split over one workgroup's waves;
+//   * gemv_valu: M <= 8 on other long matrices, on the vector ALUs.
 #include <stdlib.h>
 
 #include <atomic>
