@@ -1,8 +1,9 @@
 """Oracle: CPU restatement of the reference's hot-path op semantics.
 
 TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, always as the checker or the timed CPU
-baseline, never as the product path (the product is libhxmi.so).
+cpu_baseline leg of bench.py, always as the reference the kernels are
+compared with or as the timed CPU baseline, never as the product path (the
+product is libhxmi.so).
 
 Everything here is numpy, computed in float32 (float64 where an exact answer
 is wanted), following the reference files cited on each function.  The
