@@ -385,7 +385,7 @@ def main() -> int:
                          "calibration, and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: hexagon-mlir_amd has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
 
     import torch

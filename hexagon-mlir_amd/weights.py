@@ -288,7 +288,7 @@ def load_packed(path: str | os.PathLike, device: torch.device) -> PackedModel:
     if meta.get("format") != FORMAT:
         raise ValueError(f"{path} is not a {FORMAT} file")
     if int(meta.get("version", "0")) != VERSION:
-        raise ValueError(f"{path}: packed format version {meta.get('version')} (this build reads {VERSION})")
+        raise ValueError(f"{path}: packed format version {meta.get('version')} (this library reads {VERSION})")
     t = load_file(path, device=str(device))
     cfg = DecoderConfig(**json.loads(meta["config"]))
     idx = json.loads(meta["layer_index"])
