@@ -261,6 +261,17 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
     const bool rowok = n0 + rr < a.N;
     const uint32_t wrow = (uint32_t)(rr * a.ldw * esz + chunk * 16);
+    // this lane's two output rows: their scale and bias are fetched with the
+    // weights, not after the MFMAs (a memory round trip per tile otherwise)
+    const int n = n0 + 2 * kq;
+    float sc[2] = {1.f, 1.f}, bi[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (n + q < a.N) {
+        if (I8) sc[q] = (float)((const _Float16*)a.scale)[n + q];
+        if (a.bias) bi[q] = (float)((const _Float16*)a.bias)[n + q];
+      }
+    }
     float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j0 = 0; j0 < NWIN; j0 += U) {
@@ -292,18 +303,12 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
       }
     }
     // D[r'][m]: lane holds m = lane % 16 and A rows r' = 4 (lane / 16) + i,
-    // i.e. halves 0, 1 of weight row n0 + 2 (lane / 16) and of the next row
+    // i.e. halves 0, 1 of weight row n and of row n + 1
     const int m = lane & 15;
-    const int n = n0 + 2 * kq;
     if (m < a.M) {
       float v[2] = {acc0[0] + acc1[1], acc0[2] + acc1[3]};
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        if (n + q < a.N) {
-          if (I8) v[q] *= (float)((const _Float16*)a.scale)[n + q];
-          if (a.bias) v[q] += (float)((const _Float16*)a.bias)[n + q];
-        }
-      }
+      for (int q = 0; q < 2; ++q) v[q] = v[q] * sc[q] + bi[q];
       _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
       if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
         _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
@@ -345,6 +350,19 @@ __global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
   const uint32_t wrow = (uint32_t)(rr * a.ldw * esz + chunk * 16);
   const bool mok = rp < a.M;
   const uint32_t xbase = (uint32_t)(rp * a.ldx * 2);
+  // scale and bias of the lane's two output rows, fetched up front (wave 0
+  // applies them after the reduction)
+  const int n = n0 + 2 * kq;
+  float sc[2] = {1.f, 1.f}, bi[2] = {0.f, 0.f};
+  if (w == 0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (n + q < a.N) {
+        if (I8) sc[q] = (float)((const _Float16*)a.scale)[n + q];
+        if (a.bias) bi[q] = (float)((const _Float16*)a.bias)[n + q];
+      }
+    }
+  }
 
   float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   for (int j0 = j_begin; j0 < j_end; j0 += U) {
@@ -386,16 +404,10 @@ __global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
 #pragma unroll
   for (int q = 1; q < KS; ++q) s += red[q][lane];
   const int m = lane & 15;
-  const int n = n0 + 2 * kq;
   if (m < a.M) {
     float v[2] = {s[0], s[1]};
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      if (n + q < a.N) {
-        if (I8) v[q] *= (float)((const _Float16*)a.scale)[n + q];
-        if (a.bias) v[q] += (float)((const _Float16*)a.bias)[n + q];
-      }
-    }
+    for (int q = 0; q < 2; ++q) v[q] = v[q] * sc[q] + bi[q];
     _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
     if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
       _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
