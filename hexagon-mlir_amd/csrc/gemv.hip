@@ -321,6 +321,117 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   }
 }
 
+// gemv_pair for int8 weights, with the first tile's loads issued while x is
+// staged: x's fragments are loaded into registers first and the first
+// tile's weights right after, so the wait before storing x to LDS covers
+// the x loads only and the weights' round trip overlaps the staging (int8
+// lm_head at M = 16 29.0 -> 27.1 us on one box).  Scale and bias are one
+// 32-bit buffer load each per lane (rows n, n + 1; n is even, N % 4 == 0),
+// out of range or absent reading as zero, kept as raw bits until the
+// epilogue, so no branch makes the compiler drain the loads in flight.  The
+// fp16 kernel keeps the plain order: its compiler schedule interleaves the
+// weight loads with the MFMAs in fewer registers, and the same restructure
+// measured slower there (lm_head M = 1 40.3 -> 42.1 us).
+template <int NWIN>
+__global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
+  constexpr bool I8 = true;
+  constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
+  constexpr int FPW = I8 ? 4 : 2;     // x fragments per window
+  constexpr int CK = KW / 8;          // k per 16-byte chunk
+  constexpr int NXF = NWIN * FPW / 4; // x fragments this lane stages
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rp = lane & 15, kq = lane >> 4;
+  const int rr = rp >> 1, hh = rp & 1;
+  const int esz = I8 ? 1 : 2;
+  const int nwin = (a.K + KW - 1) / KW;
+  const int tiles = (a.N + 7) / 8;
+  const int stride = gridDim.x * 4;
+  const int chunk = hh * 4 + kq;  // this lane's 16-byte chunk of every window
+
+  // one tile's loads, all windows at once: weights, scale and bias
+  const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.scale, I8 ? (uint32_t)(a.N * 2) : 0u);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.bias, a.bias ? (uint32_t)(a.N * 2) : 0u);
+  int4v wv[NWIN];
+  uint32_t scb, bib;
+  auto fetch = [&](int tile) {
+    const int n0 = tile * 8;
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
+    const bool rowok = n0 + rr < a.N;
+    const uint32_t wrow = (uint32_t)(rr * a.ldw * esz + chunk * 16);
+#pragma unroll
+    for (int j = 0; j < NWIN; ++j) {
+      const bool ok = j < nwin && rowok && (KW * j + CK * chunk) < a.K;
+      wv[j] = load16_nt(rW, ok ? wrow + (uint32_t)(j * 128) : kOOB);
+    }
+    const uint32_t off = (uint32_t)((n0 + 2 * kq) * 2);
+    scb = I8 ? __builtin_amdgcn_raw_buffer_load_b32(rS, off, 0, 0) : 0u;
+    bib = __builtin_amdgcn_raw_buffer_load_b32(rB, off, 0, 0);
+  };
+
+  // x fragments, staged once per workgroup (the layout gemv_pair uses)
+  __shared__ __attribute__((aligned(16))) int4v xs[NWIN * FPW * 64];
+  int4v xr[NXF];
+  {
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, 0x7fffffff);
+    const bool mok = rp < a.M;
+    const uint32_t xbase = (uint32_t)(rp * a.ldx * 2);
+#pragma unroll
+    for (int i = 0; i < NXF; ++i) {
+      const int f = 4 * i + w;
+      const int j = f / FPW, q = f % FPW;
+      const int k = KW * j + (KW / 2) * (q / (FPW / 2)) + CK * kq + 8 * (q % (FPW / 2));
+      xr[i] = load16(rX, (mok && k < a.K) ? xbase + (uint32_t)(k * 2) : kOOB);
+    }
+  }
+  // (unconditional: a wave without a tile reads past N, i.e. zeros, and a
+  // branch here would make the compiler drain every load at the join)
+  int tile = blockIdx.x * 4 + w;
+  fetch(tile);
+#pragma unroll
+  for (int i = 0; i < NXF; ++i) xs[(4 * i + w) * 64 + lane] = xr[i];
+  __syncthreads();
+
+  for (bool first = true; tile < tiles; tile += stride, first = false) {
+    if (!first) fetch(tile);
+    float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NWIN; ++j) {
+      if (j < nwin) {
+        if constexpr (I8) {
+          const short8v lo = dequant8v((uint32_t)wv[j][0], (uint32_t)wv[j][1]);
+          const short8v hi = dequant8v((uint32_t)wv[j][2], (uint32_t)wv[j][3]);
+          acc0 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
+          acc0 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
+          acc1 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
+          acc1 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
+        } else {
+          const short8v wf = __builtin_bit_cast(short8v, wv[j]);
+          acc0 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
+          acc1 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
+        }
+      }
+    }
+    // D[r'][m]: lane holds m = lane % 16 and A rows r' = 4 (lane / 16) + i,
+    // i.e. halves 0, 1 of weight row n and of row n + 1
+    const int n = tile * 8 + 2 * kq;
+    const int m = lane & 15;
+    if (m < a.M) {
+      const half2v s2 = __builtin_bit_cast(half2v, scb), b2 = __builtin_bit_cast(half2v, bib);
+      const float sc0 = I8 ? (float)s2[0] : 1.f, sc1 = I8 ? (float)s2[1] : 1.f;
+      const float v[2] = {(acc0[0] + acc1[1]) * sc0 + (float)b2[0], (acc0[2] + acc1[3]) * sc1 + (float)b2[1]};
+      _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+      if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
+        _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+        *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
+      } else {
+        if (n < a.N) yrow[0] = (_Float16)v[0];
+        if (n + 1 < a.N) yrow[1] = (_Float16)v[1];
+      }
+    }
+  }
+}
+
 // Long-K GEMV (K > 1024, few rows: down projections) with the same
 // whole-line loads and row pairing: one workgroup per 8-row tile, its KS
 // waves splitting K into contiguous runs of 128-byte windows, partial sums
@@ -439,7 +550,10 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   int cap = 1024;
   if (const char* e = getenv("HXMI_GEMV_PAIR_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL((gemv_pair<I8, I8 ? 8 : 16, I8 ? 8 : 16>), dim3(blocks), dim3(256), 0, stream, v);
+  if constexpr (I8)
+    hipLaunchKernelGGL((gemv_pair_i8<8>), dim3(blocks), dim3(256), 0, stream, v);
+  else
+    hipLaunchKernelGGL((gemv_pair<false, 16, 16>), dim3(blocks), dim3(256), 0, stream, v);
   return hipGetLastError();
 }
 
