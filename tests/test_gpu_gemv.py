@@ -344,3 +344,20 @@ def test_w8a16_onehot_exact_pair_ksplit(pkg, dev, gemv_path):
     y = pkg.w8a16_linear(x.to(dev), q.to(dev), torch.ones(q.shape[0], dtype=torch.float16, device=dev))
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy().astype(np.int32), d["y"][rows])
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_w8a16_pair_ragged_rows_strided_out(pkg, dev, gemv_path, M):
+    # N % 8 == 4 (a half-empty last 8-row tile: its scale and bias loads run
+    # past N and must read zero), output rows with a leading dimension > N
+    gemv_path("pair")
+    N, K = 1004, 896
+    x = normal((M, K), 101 + M)
+    q, s = int8_weights(N, K, 102)
+    b = normal((N,), 103)
+    big = torch.full((M, 1008), 7.0, dtype=torch.float16, device=dev)
+    y = big[:, :N]
+    pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev), out=y)
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
+    assert torch.all(big[:, N:].cpu() == 7.0)  # nothing written past N
