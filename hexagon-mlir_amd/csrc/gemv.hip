@@ -16,8 +16,9 @@
 // The MFMA operand layout makes each wave instruction read 64 bytes of 16
 // rows, half cache lines.  Three more kernels read whole lines (8 rows x 128
 // bytes per wave instruction, non-temporal), which HBM serves faster:
-//   * gemv_pair: long weight matrices with K <= 1024 (the lm_head, gate/up),
-//     still on the MFMA units (each row read as two MFMA rows);
+//   * gemv_pair (fp16) / gemv_pair_i8 (int8): long weight matrices with
+//     K <= 1024 (the lm_head, gate/up), still on the MFMA units (each row
+//     read as two MFMA rows);
 //   * gemv_pair_ks: K > 1024 on at most 2048 rows (down projections), the
 //     same loads with K split over one workgroup's waves;
 //   * gemv_valu: M <= 8 on other long matrices, on the vector ALUs.
@@ -224,6 +225,8 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
 // is right for the h = 0 rows, the second for h = 1, and a row's result is
 // the sum of its two valid halves.  That doubles the MFMA work, which
 // stays a few percent of the MFMA units at HBM speed.
+// (launched for fp16 weights; int8 weights run gemv_pair_i8 below, which
+// keeps this layout and overlaps the first tile's loads with x's staging)
 template <bool I8, int NWIN, int U>
 __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
