@@ -188,3 +188,36 @@ def test_loader_errors(pkg, tmp_path):
     save_file({"x": torch.zeros(2)}, str(other), metadata={"format": "pt"})
     with pytest.raises(ValueError, match="hxmi-packed"):
         W.load_packed(other, torch.device("cpu"))
+
+
+def test_read_single_file_and_version_check(pkg, tmp_path):
+    from safetensors.torch import save_file
+
+    W = pkg.weights
+    sd = hf_state_dict(CFG_QWEN)
+    f = tmp_path / "model.safetensors"
+    save_file(sd, str(f))
+    got, cfg = W.read_checkpoint(f)
+    assert cfg is None and set(got) == set(sd)
+    inferred = W.infer_config(got, heads=4, kv_heads=1, eps=1e-6)
+    assert inferred.tie_word_embeddings and inferred.head_dim == 32 and inferred.layers == 2
+    m = W.pack_model(got, inferred, torch.device("cpu"), fold_norm=False)
+    out = tmp_path / "p.safetensors"
+    W.save_packed(out, m)
+    # a file written by a later format version is refused, not misread
+    from safetensors import safe_open
+
+    with safe_open(str(out), framework="pt") as fh:
+        meta = dict(fh.metadata())
+        tensors = {k: fh.get_tensor(k) for k in fh.keys()}
+    meta["version"] = "2"
+    save_file(tensors, str(tmp_path / "v2.safetensors"), metadata=meta)
+    with pytest.raises(ValueError, match="version 2"):
+        W.load_packed(tmp_path / "v2.safetensors", torch.device("cpu"))
+
+
+def test_int8_packing_needs_the_gpu(pkg):
+    W = pkg.weights
+    c = W.DecoderConfig.from_hf(CFG_LLAMA)
+    with pytest.raises(pkg.HxmiError, match="GPU"):
+        W.pack_model(hf_state_dict(CFG_LLAMA), c, torch.device("cpu"), fold_norm=False, int8=True)
