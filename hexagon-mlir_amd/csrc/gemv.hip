@@ -547,10 +547,12 @@ template <bool I8>
 hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   const int tiles = (v.N + 7) / 8;
   int blocks = (tiles + 3) / 4;
-  // four workgroups per CU (32 KB of staged x each), waves striding over
-  // the tiles: measured on the 896 -> 151936 lm_head, 512 / 768 / 1024 /
-  // 1280 / 2048 workgroups gave 49.3 / 47.7 / 46.5 / 55.4 / 48.5 us at M = 16
-  int cap = 1024;
+  // waves striding over the tiles, measured on the 896 -> 151936 lm_head
+  // at M = 16: fp16 four workgroups per CU (512 / 768 / 1024 / 1280 / 2048
+  // workgroups gave 49.3 / 47.7 / 46.5 / 55.4 / 48.5 us), int8 two (384 /
+  // 448 / 512 / 576 / 640 / 1024 gave 28.0 / 26.7 / 25.3 / 31.4 / 29.1 /
+  // 27.0 us: half the bytes per tile, and fewer concurrent row streams)
+  int cap = I8 ? 512 : 1024;
   if (const char* e = getenv("HXMI_GEMV_PAIR_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
   if (blocks > cap) blocks = cap;
   if constexpr (I8)
