@@ -752,12 +752,15 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   //  * whole-line MFMA kernel (K <= 1024): long weight matrices -- lm_head
   //    M = 16 54.8 -> 46.3 us and M = 4 44.0 -> 41.2 us against the other
   //    two, gate/up 896 -> 9728 at M = 16 8.3 -> 7.0 us; even at fp16
-  //    M = 1; behind row streaming for int8 at M <= 4 (lm_head 25.9 vs
-  //    22.6 us) and behind the 16-row MFMA tiles below N ~ 8192 (too few
-  //    8-row tiles to fill the GPU);
-  //  * vector-ALU row streaming: M = 1 from N = 4096, int8 M <= 4 from
-  //    N = 32768, and fp16 M <= 8 on long matrices whose K is too long for
-  //    the whole-line kernel;
+  //    M = 1; int8 at every M once N >= 16384 fills its 512 workgroups
+  //    (lm_head M = 1 / 4 21.9 / 22.1 us against 22.5 / 27.3 with row
+  //    streaming; 896 -> 32000 at M = 1 / 4 7.1 / 7.3 against 8.2 / 9.1),
+  //    int8 M <= 4 level with the other kernels below that; behind the
+  //    16-row MFMA tiles below N ~ 8192 (too few 8-row tiles to fill the
+  //    GPU);
+  //  * vector-ALU row streaming: fp16 M = 1 from N = 4096, and M <= 8
+  //    (int8 M <= 4) from N = 32768 where K is too long for the whole-line
+  //    kernel;
   //  * whole-line kernel with K split over a workgroup's waves: K > 1024
   //    on at most 2048 rows (down projections; one workgroup per 8-row
   //    tile, so at most 256 workgroups): 4864 -> 896 at M = 1 8.1 -> 5.7 us,
@@ -769,7 +772,7 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   const int64_t kpad = (p.K + kstep_v - 1) / kstep_v * kstep_v;
   const bool fits = p.M <= 16 && p.M * kpad * 2 <= 64 * 1024;
   const bool xfits = p.K <= 1024;
-  g.pair = xfits && p.N >= 8192 && (!p.w_int8 || p.M > 4);
+  g.pair = xfits && p.N >= 8192 && (!p.w_int8 || p.M > 4 || p.N >= 16384);
   g.pair_ks = !xfits && p.N <= 2048;
   if (g.pair_ks) {
     const int64_t nwin = (p.K + (p.w_int8 ? 127 : 63)) / (p.w_int8 ? 128 : 64);
