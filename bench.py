@@ -341,18 +341,19 @@ def profile_suite(pkg, torch, dev, timer) -> None:
         timer._warm(gemv)
         for i in range(5):
             gemv(i)
-    x = torch.randn(1, H, generator=g).half().to(dev)
-    y = torch.empty(1, V, dtype=torch.float16, device=dev)
-    w8 = lambda i=0: pkg.w8a16_linear(x, qs[i % 3], sc, out=y)
-    timer._warm(w8)
-    for i in range(5):
-        w8(i)
+    for M in (1, 16):
+        x = torch.randn(M, H, generator=g).half().to(dev)
+        y = torch.empty(M, V, dtype=torch.float16, device=dev)
+        w8 = lambda i=0: pkg.w8a16_linear(x, qs[i % 3], sc, out=y)
+        timer._warm(w8)
+        for i in range(5):
+            w8(i)
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log("[bench] profile suite: 4096^3 GEMM, lm_head GEMV fp16 M=1/16, int8 M=1, 5 x 256 MiB copies")
+    log("[bench] profile suite: 4096^3 GEMM, lm_head GEMV fp16 M=1/16, int8 M=1/16, 5 x 256 MiB copies")
 
 
 def traffic_from_profiles():
