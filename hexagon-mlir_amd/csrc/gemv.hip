@@ -227,7 +227,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
 // stays a few percent of the MFMA units at HBM speed.
 // (launched for fp16 weights; int8 weights run gemv_pair_i8 below, which
 // keeps this layout and overlaps the first tile's loads with x's staging)
-template <bool I8, int NWIN, int U>
+template <bool I8, int NWIN, int U, int YKEEP>
 __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
   constexpr int FPW = I8 ? 4 : 2;     // x fragments per window
@@ -259,7 +259,25 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   __syncthreads();
 
   const int chunk = hh * 4 + kq;  // this lane's 16-byte chunk of every window
-  for (int tile = blockIdx.x * 4 + w; tile < tiles; tile += gridDim.x * 4) {
+  // The y pair of each of this wave's first YKEEP tiles waits in LDS and is
+  // stored after the last tile, so y's scattered 16-byte pieces do not
+  // interleave with the weight stream (lm_head M = 16 46.9 -> 44.6-45.2 us;
+  // at M = 1, where y is 0.3 MB, deferring cost 0.6 us and YKEEP is 0).
+  __shared__ uint32_t ykeep[4][YKEEP > 0 ? YKEEP : 1][64];
+  const int m = lane & 15;
+  auto store_pair = [&](int n, uint32_t bits) {
+    _Float16 h2[2];
+    __builtin_memcpy(h2, &bits, 4);
+    _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+    if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
+      *(uint32_t*)yrow = bits;
+    } else {
+      if (n < a.N) yrow[0] = h2[0];
+      if (n + 1 < a.N) yrow[1] = h2[1];
+    }
+  };
+  int it = 0;
+  for (int tile = blockIdx.x * 4 + w; tile < tiles; tile += gridDim.x * 4, ++it) {
     const int n0 = tile * 8;
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)n0 * a.ldw * esz, 0x7fffffff);
     const bool rowok = n0 + rr < a.N;
@@ -307,20 +325,19 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
     }
     // D[r'][m]: lane holds m = lane % 16 and A rows r' = 4 (lane / 16) + i,
     // i.e. halves 0, 1 of weight row n and of row n + 1
-    const int m = lane & 15;
-    if (m < a.M) {
+    {
       float v[2] = {acc0[0] + acc1[1], acc0[2] + acc1[3]};
 #pragma unroll
       for (int q = 0; q < 2; ++q) v[q] = v[q] * sc[q] + bi[q];
-      _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
-      if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
-        _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
-        *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
-      } else {
-        if (n < a.N) yrow[0] = (_Float16)v[0];
-        if (n + 1 < a.N) yrow[1] = (_Float16)v[1];
-      }
+      _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+      const uint32_t bits = __builtin_bit_cast(uint32_t, h2);
+      if (YKEEP > 0 && it < YKEEP) ykeep[w][it][lane] = bits;
+      else if (m < a.M) store_pair(n, bits);
     }
+  }
+  if (YKEEP > 0 && m < a.M) {
+    for (int i = 0; i < it && i < YKEEP; ++i)
+      store_pair((blockIdx.x * 4 + w + i * gridDim.x * 4) * 8 + 2 * kq, ykeep[w][i][lane]);
   }
 }
 
@@ -557,8 +574,10 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   if (blocks > cap) blocks = cap;
   if constexpr (I8)
     hipLaunchKernelGGL((gemv_pair_i8<8>), dim3(blocks), dim3(256), 0, stream, v);
+  else if (v.M > 4)
+    hipLaunchKernelGGL((gemv_pair<false, 16, 16, 6>), dim3(blocks), dim3(256), 0, stream, v);
   else
-    hipLaunchKernelGGL((gemv_pair<false, 16, 16>), dim3(blocks), dim3(256), 0, stream, v);
+    hipLaunchKernelGGL((gemv_pair<false, 16, 16, 0>), dim3(blocks), dim3(256), 0, stream, v);
   return hipGetLastError();
 }
 
