@@ -14,8 +14,8 @@ Secondary lines in the same JSON object (``secondary``): the 1024^3 and
 weight-only, rotating weight copies past the 256 MB Infinity Cache), a
 whole 24-layer decode step, RMSNorm, softmax and the ViT-B/16 block.
 
-``cpu_baseline`` times the oracle (numpy fp32, the reference's CPU-path
-semantics) on the host cores for a bounded sample of the same block.
+``cpu_baseline`` times the reference's own CPU path (PyTorch CPU ops in
+fp32) on the same block, on the host's allowed threads and on one thread.
 """
 from __future__ import annotations
 
@@ -29,8 +29,9 @@ import time
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-PEAK_FP16_TFLOPS = 2516.6  # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
-PEAK_HBM_GBS = 8000.0
+ROOFLINE = json.loads((ROOT / "config" / "roofline.json").read_text())
+PEAK_FP16_TFLOPS = ROOFLINE["peak_fp16_tflops"]  # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
+PEAK_HBM_GBS = ROOFLINE["peak_hbm_gbs"]
 
 TL_M, TL_H, TL_QKV, TL_I = 512, 2048, 2560, 5632
 
@@ -160,8 +161,82 @@ def make_block(pkg, torch, dev):
     def gate_up(_i=0):
         pkg.rms_norm_linear(x, wgu_f, 1e-5, epilogue="silu_mul", out=buf["h"], rscale_in=buf["rs"])
 
-    tensors = dict(x=x, gn=gn, wqkv=wqkv, wo=wo, wg=wg, wu=wu, wd=wd, xa=xa, step_unfused=step_unfused)
+    tensors = dict(x=x, gn=gn, wqkv=wqkv, wo=wo, wg=wg, wu=wu, wd=wd, xa=xa, wqkv_f=wqkv_f, wgu_f=wgu_f,
+                   step_unfused=step_unfused)
     return step, gate_up, tensors, buf
+
+
+def check_block(torch, t, buf, tol: float = 1e-2) -> dict:
+    """One TinyLlama block step's outputs against a plain torch fp32
+    computation of the same block on the GPU (RMSNorm in fp32 with the folded
+    weights, fp32 matmuls, SiLU-mul, the down projection of the kernel's own
+    fp16 h): max relative error per output, floor 1e-3 of its RMS."""
+    f = lambda v: v.float()  # noqa: E731
+    xn = f(t["x"]) * torch.rsqrt(f(t["x"]).pow(2).mean(-1, keepdim=True) + 1e-5)
+    exp = {"qkv": xn @ f(t["wqkv_f"]).t(), "o": f(t["xa"]) @ f(t["wo"]).t()}
+    gu = xn @ f(t["wgu_f"]).t()  # packed columns: [32q, 32q+16) gate, [32q+16, 32q+32) up
+    gu = gu.reshape(gu.shape[0], -1, 2, 16)
+    exp["h"] = (torch.nn.functional.silu(gu[:, :, 0]) * gu[:, :, 1]).reshape(gu.shape[0], -1)
+    exp["d"] = f(buf["h"]) @ f(t["wd"]).t()
+    return {k: rel_err(torch, buf[k], v) for k, v in exp.items()}
+
+
+def rel_err(torch, out, exp, vs_scale: bool = False) -> float:
+    """max |out - exp| / max(|exp|, 1e-3 * rms(exp)), on the device; with
+    vs_scale, max |out - exp| / max |exp| (for attention, whose fp16
+    probabilities leave ~1e-4 absolute noise at outputs that average to ~0)."""
+    out, exp = out.float(), exp.float()
+    if not bool(torch.isfinite(out).all()):
+        return float("inf")
+    if vs_scale:
+        return float((out - exp).abs().max() / exp.abs().max().clamp_min(1e-30))
+    floor = max(1e-3 * float(exp.pow(2).mean().sqrt()), 1e-30)
+    return float(((out - exp).abs() / exp.abs().clamp_min(floor)).max())
+
+
+VIT_B, VIT_S, VIT_H, VIT_D, VIT_E, VIT_F = 8, 197, 12, 64, 768, 3072
+
+
+def make_vit(pkg, torch, dev):
+    """ViT-B/16-shaped attention + MLP, batch 8, fp16: Q/K/V [96, 197, 64] ~
+    N(0,1), SDPA with scale 1/8; x [1576, 768] ~ N(0,1) -> fc1 768->3072 +
+    bias + tanh-GELU -> fc2 3072->768 + bias, weights and biases N(0,0.02)."""
+    g = torch.Generator().manual_seed(5)
+    B, S, Hh, D, E, F = VIT_B, VIT_S, VIT_H, VIT_D, VIT_E, VIT_F
+    t = {
+        "q": torch.randn(B * Hh, S, D, generator=g).half().to(dev),
+        "k": torch.randn(B * Hh, S, D, generator=g).half().to(dev),
+        "v": torch.randn(B * Hh, S, D, generator=g).half().to(dev),
+        "x": torch.randn(B * S, E, generator=g).half().to(dev),
+        "w1": (torch.randn(F, E, generator=g) * 0.02).half().to(dev),
+        "b1": (torch.randn(F, generator=g) * 0.02).half().to(dev),
+        "w2": (torch.randn(E, F, generator=g) * 0.02).half().to(dev),
+        "b2": (torch.randn(E, generator=g) * 0.02).half().to(dev),
+    }
+    buf = {"attn": torch.empty(B * Hh, S, D, dtype=torch.float16, device=dev),
+           "h": torch.empty(B * S, F, dtype=torch.float16, device=dev),
+           "y": torch.empty(B * S, E, dtype=torch.float16, device=dev)}
+
+    def attention(_i=0):
+        pkg.attention(t["q"], t["k"], t["v"], 0.125, out=buf["attn"])
+
+    def step(_i=0):
+        attention()
+        pkg.linear(t["x"], t["w1"], t["b1"], epilogue="gelu_tanh", out=buf["h"])
+        pkg.linear(buf["h"], t["w2"], t["b2"], out=buf["y"])
+
+    return step, attention, t, buf
+
+
+def check_vit(torch, t, buf) -> dict:
+    """The ViT step's outputs against torch fp32 on the GPU: SDPA in fp32,
+    fc1 + bias + tanh-GELU, fc2 + bias of the kernel's own fp16 h."""
+    f = lambda v: v.float()  # noqa: E731
+    s = torch.bmm(f(t["q"]), f(t["k"]).transpose(1, 2).contiguous()) * 0.125
+    exp = {"attn": torch.bmm(torch.softmax(s, -1), f(t["v"]))}
+    exp["h"] = torch.nn.functional.gelu(f(t["x"]) @ f(t["w1"]).t() + f(t["b1"]), approximate="tanh")
+    exp["y"] = f(buf["h"]) @ f(t["w2"]).t() + f(t["b2"])
+    return {k: rel_err(torch, buf[k], v, vs_scale=(k == "attn")) for k, v in exp.items()}
 
 
 def bench_gemm(pkg, torch, dev, timer, M, N, K, layout, iters):
@@ -176,28 +251,36 @@ def bench_gemm(pkg, torch, dev, timer, M, N, K, layout, iters):
 
 
 def bench_gemv(pkg, torch, dev, timer, M, K, N, int8, iters, min_bytes=768 << 20):
-    """GB/s of one decode linear with enough distinct weight copies in the
-    rotation that no copy is still cached when it is read again."""
+    """One decode linear, rotating over enough distinct weight copies (>= 768
+    MB in all, three times the 256 MB Infinity Cache) that no copy is still
+    cached when it is read again; each graph replay reads every copy once.
+    GB/s against the HBM peak; for M > 16 (near the ridge) also TFLOP/s
+    against min(MFMA peak, arithmetic intensity x HBM peak)."""
     g = torch.Generator().manual_seed(2)
     wbytes = N * K * (1 if int8 else 2)
     copies = max(2, -(-min_bytes // wbytes))
-    copies = min(copies, 64)
     x = torch.randn(M, K, generator=g).half().to(dev)
     y = torch.empty(M, N, dtype=torch.float16, device=dev)
     if int8:
-        ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev) for _ in range(copies)]
+        ws = torch.randint(-127, 128, (copies, N, K), dtype=torch.int8, device=dev)
         s = (torch.rand(N, generator=g) * 9e-3 + 1e-3).half().to(dev)
         fn = lambda i: pkg.w8a16_linear(x, ws[i % copies], s, out=y)  # noqa: E731
         algo = N * K + 2 * N + 2 * M * K + 2 * M * N
     else:
-        ws = [torch.empty(N, K, dtype=torch.float16, device=dev).normal_(0, 0.02) for _ in range(copies)]
+        ws = torch.empty(copies, N, K, dtype=torch.float16, device=dev).normal_(0, 0.02)
         fn = lambda i: pkg.gemv(x, ws[i % copies], out=y)  # noqa: E731
         algo = 2 * (N * K + M * K + M * N)
-    ms = timer.graph_ms(fn, max(iters, 2 * copies))
+    ms = timer.graph_ms(fn, max(iters, copies))
     gbs = algo / (ms * 1e-3) / 1e9
     del ws
-    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-            "bytes": algo, "weight_copies": copies}
+    out = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+           "bytes": algo, "weight_copies": copies}
+    if M > 16:
+        flop = 2 * M * N * K
+        tf = flop / (ms * 1e-3) / 1e12
+        bound = min(PEAK_FP16_TFLOPS, flop / algo * PEAK_HBM_GBS / 1e3)
+        out.update({"tflops": round(tf, 1), "roofline_tflops": round(bound, 1), "frac_roofline": round(tf / bound, 4)})
+    return out
 
 
 def bench_decode_step(pkg, torch, dev, timer, iters):
@@ -251,71 +334,87 @@ def bench_rows(pkg, torch, dev, timer, iters):
 
 
 def bench_vit(pkg, torch, dev, timer, iters):
-    g = torch.Generator().manual_seed(5)
-    B, S, Hh, D, E, F = 8, 197, 12, 64, 768, 3072
-    q = torch.randn(B * Hh, S, D, generator=g).half().to(dev)
-    k = torch.randn(B * Hh, S, D, generator=g).half().to(dev)
-    v = torch.randn(B * Hh, S, D, generator=g).half().to(dev)
-    x = torch.randn(B * S, E, generator=g).half().to(dev)
-    w1 = (torch.randn(F, E, generator=g) * 0.02).half().to(dev)
-    b1 = (torch.randn(F, generator=g) * 0.02).half().to(dev)
-    w2 = (torch.randn(E, F, generator=g) * 0.02).half().to(dev)
-    b2 = (torch.randn(E, generator=g) * 0.02).half().to(dev)
-
-    def step(_i=0):
-        pkg.attention(q, k, v, 0.125)
-        h = pkg.linear(x, w1, b1, epilogue="gelu_tanh")
-        pkg.linear(h, w2, b2)
-
+    step, attention, t, buf = make_vit(pkg, torch, dev)
+    B, S, Hh, D, E, F = VIT_B, VIT_S, VIT_H, VIT_D, VIT_E, VIT_F
+    step()
+    torch.cuda.synchronize()
+    errs = check_vit(torch, t, buf)
+    log(f"[bench] ViT check vs torch fp32: {errs}")
+    if max(errs.values()) > 1e-2:
+        raise SystemExit("[bench] FAILED: the ViT block's outputs differ from the fp32 reference by more than 1e-2")
     ms = timer.graph_ms(step, iters)
     flops = 2 * (2 * B * Hh * S * S * D) + 2 * (2 * B * S * E * F)
-    att_ms = timer.graph_ms(lambda _i=0: pkg.attention(q, k, v, 0.125), iters)
+    att_ms = timer.graph_ms(attention, iters)
     att_flops = 2 * (2 * B * Hh * S * S * D)
     att_bytes = 4 * B * Hh * S * D * 2  # Q, K, V read once, O written once
     return {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
             "attention_us": round(att_ms * 1e3, 2), "attention_tflops": round(att_flops / (att_ms * 1e-3) / 1e12, 1),
-            "attention_gbs": round(att_bytes / (att_ms * 1e-3) / 1e9, 1)}
+            "attention_gbs": round(att_bytes / (att_ms * 1e-3) / 1e9, 1),
+            "attention_frac_hbm_peak": round(att_bytes / (att_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
-def cpu_baseline(budget_s: float = 12.0) -> dict:
-    """The oracle (numpy fp32) running the same prefill block on host cores,
-    repeated until about budget_s seconds of CPU work."""
-    import numpy as np
-
-    from oracle import hot_path as ref
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover - threadpoolctl is optional
-        threads = os.cpu_count() or 1
-    r = np.random.default_rng(0)
-    x = r.standard_normal((TL_M, TL_H)).astype(np.float16)
-    gn = (1 + 0.02 * r.standard_normal(TL_H)).astype(np.float16)
-    wqkv = (0.02 * r.standard_normal((TL_QKV, TL_H))).astype(np.float16)
-    wo = (0.02 * r.standard_normal((TL_H, TL_H))).astype(np.float16)
-    wg = (0.02 * r.standard_normal((TL_I, TL_H))).astype(np.float16)
-    wu = (0.02 * r.standard_normal((TL_I, TL_H))).astype(np.float16)
-    wd = (0.02 * r.standard_normal((TL_H, TL_I))).astype(np.float16)
-    xa = r.standard_normal((TL_M, TL_H)).astype(np.float16)
+
+def cpu_baseline(runs: int = 7) -> dict:
+    """The reference's CPU path for the headline block: PyTorch CPU ops in
+    fp32 (the x86 forward its benchmarks compare against,
+    benchmark_models/run_tinyllama.py:204-205,
+    micro_bench/test_matmul_benchmark.py:91) -- RMSNorm, the QKV, O, gate,
+    up and down linears and SiLU-mul of the 512-token TinyLlama block on the
+    same-shaped seeded inputs -- timed on this host with every thread torch
+    is allowed (OMP_NUM_THREADS) and with one thread: median of `runs` blocks
+    after one warm-up block each."""
+    import torch
+    import torch.nn.functional as F
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(TL_M, TL_H, generator=g)
+    gn = 1 + 0.02 * torch.randn(TL_H, generator=g)
+    wqkv = 0.02 * torch.randn(TL_QKV, TL_H, generator=g)
+    wo = 0.02 * torch.randn(TL_H, TL_H, generator=g)
+    wg = 0.02 * torch.randn(TL_I, TL_H, generator=g)
+    wu = 0.02 * torch.randn(TL_I, TL_H, generator=g)
+    wd = 0.02 * torch.randn(TL_H, TL_I, generator=g)
+    xa = torch.randn(TL_M, TL_H, generator=g)
 
     def block():
-        xn = ref.rms_norm(x, gn, 1e-5).astype(np.float16)
-        ref.linear(xn, wqkv)
-        ref.linear(xa, wo)
-        h = ref.silu_mul_linear(xn, wg, wu).astype(np.float16)
-        ref.linear(h, wd)
+        xn = F.rms_norm(x, (TL_H,), gn, 1e-5)
+        F.linear(xn, wqkv)
+        F.linear(xa, wo)
+        h = F.silu(F.linear(xn, wg)) * F.linear(xn, wu)
+        F.linear(h, wd)
 
-    block()
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s or n < 2:
-        block()
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    tf = tinyllama_flops()["total"] / dt / 1e12
-    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": f"{n} passes of the full 512-token TinyLlama block (fp32 numpy oracle), {dt * 1e3:.1f} ms each"}
+    def median_ms(threads: int) -> float:
+        torch.set_num_threads(threads)
+        times = []
+        with torch.no_grad():
+            block()
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                block()
+                times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2] * 1e3
+
+    all_threads = torch.get_num_threads()
+    ms_all = median_ms(all_threads)
+    ms_one = median_ms(1)
+    torch.set_num_threads(all_threads)
+    flop = tinyllama_flops()["total"]
+    tf = lambda ms: round(flop / (ms * 1e-3) / 1e12, 4)  # noqa: E731
+    return {"value": tf(ms_all), "unit": "TFLOP/s", "cores": int(all_threads), "kind": "reference",
+            "sample": f"the reference's CPU path: torch {torch.__version__} CPU fp32 ops of the full 512-token "
+                      f"TinyLlama block (RMSNorm, QKV, O, gate/up + SiLU-mul, down), median of {runs} blocks "
+                      f"after a warm-up, {ms_all:.1f} ms each on {all_threads} threads",
+            "median_ms": round(ms_all, 2), "single_thread": {"value": tf(ms_one), "median_ms": round(ms_one, 2)},
+            "cpu_model": _cpu_model(), "host_cpus": os.cpu_count(), "torch": torch.__version__}
 
 
 def profile_suite(pkg, torch, dev, timer) -> None:
@@ -402,8 +501,16 @@ def main() -> int:
     if args.profile_suite:
         profile_suite(pkg, torch, dev, timer)
         return 0
-    step, gate_up, block_tensors, _ = make_block(pkg, torch, dev)
+    step, gate_up, block_tensors, block_buf = make_block(pkg, torch, dev)
     fl = tinyllama_flops()
+    # one step checked against torch fp32 before anything is timed
+    step()
+    torch.cuda.synchronize()
+    errs = check_block(torch, block_tensors, block_buf)
+    log(f"[bench] block check vs torch fp32 (max rel err): {errs}")
+    if max(errs.values()) > 1e-2:
+        log("[bench] FAILED: the block's outputs differ from the fp32 reference by more than 1e-2")
+        return 3
     if args.profile:
         step()
         for _ in range(args.steps):

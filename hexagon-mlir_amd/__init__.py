@@ -28,7 +28,9 @@ from .hxmi import (
     quantize_int8,
     rms_norm,
     rms_norm_linear,
+    set_tuning,
     softmax,
+    tuning,
     w8a16_linear,
 )
 
@@ -49,6 +51,8 @@ __all__ = [
     "quantize_int8",
     "rms_norm",
     "rms_norm_linear",
+    "set_tuning",
     "softmax",
+    "tuning",
     "w8a16_linear",
 ]

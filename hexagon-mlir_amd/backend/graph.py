@@ -129,6 +129,16 @@ class Plan:
     module: fx.GraphModule
     kernels: list = field(default_factory=list)  # (pattern, node name)
     torch_ops: list = field(default_factory=list)  # aten ops left to torch
+    gemm_tile: Optional[int] = None  # GEMM tile forced for this plan's runs (tileSizes), else the picker's
+
+    def __call__(self, *args):
+        """Run the planned module.  A forced tile steers only the GEMMs of this
+        run (a thread-local override, restored afterwards), as the
+        reference's tileSizes option applies to one compilation."""
+        if self.gemm_tile is None:
+            return self.module(*args)
+        with _pkg().tuning(gemm_tile=self.gemm_tile):
+            return self.module(*args)
 
     def summary(self) -> str:
         lines = [f"hxmi kernels: {len(self.kernels)}"]
@@ -392,8 +402,11 @@ class _Planner:
         return self.plan
 
 
-def plan_program(program: Any, device: torch.device, fusion: bool = True) -> Plan:
-    """Plan an ExportedProgram (or a GraphModule) for execution on `device`."""
+def plan_program(program: Any, device: torch.device, fusion: bool = True, gemm_tile: Optional[int] = None) -> Plan:
+    """Plan an ExportedProgram (or a GraphModule) for execution on `device`;
+    gemm_tile forces the GEMM tile (TileId) of the plan's runs."""
     gm = program.module() if hasattr(program, "module") else program
     gm = gm.to(device)
-    return _Planner(gm, fusion).run()
+    plan = _Planner(gm, fusion).run()
+    plan.gemm_tile = gemm_tile
+    return plan

@@ -13,7 +13,6 @@ Test_Info report and timestamped artifact folder.
 """
 from __future__ import annotations
 
-import json
 import os
 import shutil
 import time
@@ -64,9 +63,8 @@ class TorchMLIRHexagonLauncher(HexagonLauncherBase):
         summary is written to <func_name>.plan.txt in the artifact folder."""
         opts = options_from_dict(options)
         program = torch.export.load(mlir_bytecode_path)
-        if opts.tileSizes:
-            os.environ["HXMI_GEMM_TILE"] = str(_tile_id(opts.tileSizes))
-        plan = plan_program(program, self.device, fusion=opts.fusion)
+        tile = _tile_id(opts.tileSizes) if opts.tileSizes else None
+        plan = plan_program(program, self.device, fusion=opts.fusion, gemm_tile=tile)
         if opts.lowerConstantsInSeparateSharedObjects:
             self._constants_artifact(plan, local_dir, func_name)
         with open(os.path.join(local_dir, f"{func_name}.plan.txt"), "w") as f:
@@ -123,16 +121,15 @@ class TorchMLIRHexagonLauncher(HexagonLauncherBase):
         (HIP events), the Test_Info report, outputs as CPU tensors (also
         written to <func_name>_o<i>.raw in the reference's output format)."""
         args = [x.to(self.device) if isinstance(x, torch.Tensor) else x for x in inputs]
-        gm = plan.module
         with torch.no_grad():
-            outs = gm(*args)
+            outs = plan(*args)
             torch.cuda.synchronize(self.device)
             iters = max(int(iterations), 1)
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
             s.record()
             for _ in range(iters):
-                outs = gm(*args)
+                outs = plan(*args)
             e.record()
             torch.cuda.synchronize(self.device)
         self.report(local_dir, "_mlir_ciface_" + func_name, s.elapsed_time(e) * 1e3 / iters)
@@ -147,30 +144,50 @@ class TorchMLIRHexagonLauncher(HexagonLauncherBase):
         return results
 
     def _per_op_timing(self, plan: Plan, args: list, local_dir: str) -> None:
-        """GPU time of every node (HIP events around it), as lwp.json."""
+        """Region timing of one run in the reference's LWP files: region 0 is
+        the whole function, region i >= 1 the i-th op of the planned graph;
+        begin and end markers on the GPU stream bracket each region's kernels
+        (lwp.json), and lwp_infodump.txt maps each id to the op's position in
+        the graph and its name."""
         from torch.fx import Interpreter
 
-        times = []
+        from .lwp import LwpRecorder, write_lwp
 
-        class Timed(Interpreter):
+        ops = [n for n in plan.module.graph.nodes if n.op in ("call_function", "call_module")]
+        ids = {n: i + 1 for i, n in enumerate(ops)}
+        positions = {n: i for i, n in enumerate(plan.module.graph.nodes)}
+        rec = LwpRecorder(self.device, capacity=2 * len(ops) + 2)
+
+        class Marked(Interpreter):
             def run_node(self, n):
-                if n.op not in ("call_function", "call_module"):
+                if n not in ids:
                     return super().run_node(n)
-                s = torch.cuda.Event(enable_timing=True)
-                e = torch.cuda.Event(enable_timing=True)
-                s.record()
+                rec.mark(ids[n])
                 r = super().run_node(n)
-                e.record()
-                times.append((n, s, e))
+                rec.mark(ids[n])
                 return r
 
         with torch.no_grad():
-            Timed(plan.module).run(*args)
-        torch.cuda.synchronize(self.device)
-        rows = [{"node": n.name, "target": str(n.target), "us": round(s.elapsed_time(e) * 1e3, 3)}
-                for n, s, e in times]
-        with open(os.path.join(local_dir, "lwp.json"), "w") as f:
-            json.dump(rows, f, indent=1)
+            ctx = self._tile_scope(plan)
+            with ctx:
+                rec.mark(0)
+                Marked(plan.module).run(*args)
+                rec.mark(0)
+        regions = [(0, [0], ["func"])]
+        regions += [(ids[n], [positions[n]], [n.name + ": " + getattr(n.target, "__name__", str(n.target))])
+                    for n in ops]
+        write_lwp(os.path.join(local_dir, "lwp.json"), os.path.join(local_dir, "lwp_infodump.txt"), rec.entries(),
+                  rec.clock_hz(), regions)
+
+    @staticmethod
+    def _tile_scope(plan: Plan):
+        import contextlib
+
+        if plan.gemm_tile is None:
+            return contextlib.nullcontext()
+        from .. import hxmi
+
+        return hxmi.tuning(gemm_tile=plan.gemm_tile)
 
 
 def _tile_id(tile_sizes: str) -> int:

@@ -115,7 +115,15 @@ extern "C" {
 
 const char* hxmi_last_error(void) { return g_err; }
 
-int hxmi_version(void) { return 100; }
+int hxmi_version(void) { return 200; }
+
+int hxmi_set_tuning(const char* name, int64_t value, int64_t* previous) {
+  const int k = hxmi::knob_index(name);
+  REQUIRE(k >= 0, "hxmi_set_tuning: unknown knob %s", name ? name : "(null)");
+  const int64_t prev = hxmi::set_knob_override(k, value);
+  if (previous) *previous = prev;
+  return ok();
+}
 
 int hxmi_gemm_f16(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
                   int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha, void* workspace,
@@ -352,6 +360,21 @@ int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, in
   REQUIRE((uintptr_t)W % 16 == 0 && (uintptr_t)q % 8 == 0 && (uintptr_t)s % 2 == 0,
           "%s: W must be 16-byte, q 8-byte aligned", name);
   return from_hip(hxmi::launch_quantize_int8_rows(W, q, s, N, K, ldw, ldq, (hipStream_t)stream), name);
+}
+
+int hxmi_lwp_record(uint32_t* records, int64_t slot, uint32_t id, void* stream) {
+  const char* name = "hxmi_lwp_record";
+  REQUIRE(records, "%s: null record buffer", name);
+  REQUIRE(slot >= 0, "%s: negative slot", name);
+  REQUIRE((uintptr_t)records % 4 == 0, "%s: record buffer must be 4-byte aligned", name);
+  return from_hip(hxmi::launch_lwp_mark(records, slot, id, (hipStream_t)stream), name);
+}
+
+int64_t hxmi_lwp_clock_hz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return 0;
+  return (int64_t)khz * 1000;
 }
 
 int hexkl_matmul_f16f16_f32(int64_t n_row, int64_t n_col, int64_t n_inner, float* outM, const hxmi_f16_t* inAct,

@@ -1,10 +1,6 @@
 // GEMM dispatch: alignment checks, tile choice, and the element-wise kernel
 // used for operands the MFMA fast path cannot take (odd strides, K or N not a
 // multiple of 8, misaligned pointers).
-#include <stdlib.h>
-
-#include <atomic>
-
 #include "gemm_impl.h"
 
 namespace hxmi {
@@ -87,9 +83,10 @@ __global__ __launch_bounds__(256) void gemm_elementwise(GArgs a) {
     ((T*)a.C)[b * a.sC + m * a.ldc + o] = (T)v;
 }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : dflt;
+// a knob's value, or dflt when unset
+int knob_or(Knob k, int dflt) {
+  const int64_t v = knob(k);
+  return v == KNOB_UNSET ? dflt : (int)v;
 }
 
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
@@ -158,7 +155,7 @@ namespace gemm {
 namespace {
 
 int tile_for(const GemmProblem& p) {
-  int tile = p.tile >= 0 ? p.tile : env_int("HXMI_GEMM_TILE", -1);
+  int tile = p.tile >= 0 ? p.tile : knob_or(KNOB_GEMM_TILE, -1);
   if (tile < 0 || tile >= TILE_COUNT) tile = gemm_pick_tile(p);
   if (p.epilogue == EPI_SILU_MUL && kTiles[tile].BN < 128) tile = TILE_64x128;
   return tile;
@@ -185,7 +182,7 @@ KArgs make_kargs(const GemmProblem& p, int tile) {
   k.alpha = p.alpha;
   k.tiles_m = (int)((p.M + s.BM - 1) / s.BM);
   k.tiles_n = (int)((p.N + s.BN - 1) / s.BN);
-  const int gm = env_int("HXMI_GROUP_M", 4);
+  const int gm = knob_or(KNOB_GROUP_M, 4);
   k.group_m = gm < 1 ? 1 : (gm > k.tiles_m ? k.tiles_m : gm);
   k.k_last = 0;
   k.rms_eps = p.rms_eps;
@@ -217,7 +214,7 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 // projection at M = 256: 105 -> 128 TFLOP/s).
 int gemm_splits(const GemmProblem& p) {
   if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || !gemm_fast_path_ok(p)) return 1;
-  if (const char* e = getenv("HXMI_SPLITK")) return atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
+  if (const int64_t e = knob(KNOB_SPLITK); e != KNOB_UNSET) return e < 1 ? 1 : (e > 16 ? 16 : (int)e);
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 127) / 128);
   if (tiles >= 384 || p.K < 3072) return 1;
   // long slices: two of them once every CU has a workgroup (measured in the
@@ -244,12 +241,12 @@ static bool split_plan(const GemmProblem& p, GemmProblem& q, int& tile, int64_t&
   q.sA = kc;
   q.sB = p.b_nt ? kc : kc * p.ldb;
   q.sC = 0;
-  if (q.tile < 0 && gemm::env_int("HXMI_GEMM_TILE", -1) < 0) q.tile = p.dtype == DT_W8A16 ? TILE_64x64 : TILE_64x128;
+  if (q.tile < 0 && gemm::knob_or(KNOB_GEMM_TILE, -1) < 0) q.tile = p.dtype == DT_W8A16 ? TILE_64x64 : TILE_64x128;
   tile = gemm::tile_for(q);
   const gemm::TileShape s = gemm::kTiles[tile];
   const int64_t tiles = ((p.M + s.BM - 1) / s.BM) * ((p.N + s.BN - 1) / s.BN);
-  need = gemm::fix_counter_bytes(tiles) + tiles * q.batch * s.BM * s.BN * 4;
-  return q.batch > 1;
+  need = kWsCounterBytes + tiles * q.batch * s.BM * s.BN * 4;
+  return q.batch > 1 && tiles <= kWsMaxTiles;
 }
 
 int64_t gemm_workspace_bytes(const GemmProblem& p) {
@@ -304,11 +301,9 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream) {
   if (split_plan(p, q, qtile, need) && p.ws && p.ws_bytes >= need && ((uintptr_t)p.ws % 256) == 0) {
     // K slices as a batch into one output; the last slice to finish a tile
     // adds the fp32 partials (in the workspace) and runs the epilogue
-    static std::atomic<unsigned long long> calls{1};
     gemm::KArgs k = gemm::make_kargs(q, qtile);
     k.k_last = (int)(p.K - (q.batch - 1) * q.K);
     k.fix = (char*)p.ws;
-    k.epoch = calls.fetch_add(1) & ((1ull << 56) - 1);
     return gemm::launch_fast(q, qtile, k, stream);
   }
 
@@ -334,7 +329,7 @@ GemmProblem w8a16_as_gemm(const GemvProblem& p) {
   q.dtype = DT_W8A16;
   q.b_nt = 1;
   q.epilogue = p.bias ? EPI_BIAS : EPI_NONE;
-  q.tile = gemm::env_int("HXMI_W8_TILE", -1);
+  q.tile = gemm::knob_or(KNOB_W8_TILE, -1);
   return q;
 }
 

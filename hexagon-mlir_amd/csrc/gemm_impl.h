@@ -44,17 +44,16 @@ struct KArgs {
   int k_last;  // > 0: the last batch entry has this K (split-K: a ragged last slice)
   float rms_eps;  // RMS kernels: epsilon of the row RMSNorm folded into the GEMM
   // Split-K with in-kernel fix-up (fix != nullptr): the batch entries are K
-  // slices of one output (sC = 0).  fix holds one arrival counter per output
-  // tile, then batch fp32 partial tiles per output tile in fragment order;
-  // epoch tags the call so counters left by other calls read as zero.
+  // slices of one output (sC = 0).  fix holds one 64-bit arrival counter per
+  // output tile in its first kWsCounterBytes, then batch fp32 partial tiles
+  // per output tile in fragment order.  The counters must be zero when the
+  // launch starts; the last slice to arrive at a tile resets its counter to
+  // zero, so every launch leaves them zero for the next one.
   char* fix;
-  unsigned long long epoch;
   float* rs_out;       // RMS kernels: row scales rsqrt(mean + eps) written here (optional)
   const float* rs_in;  // other kernels: row scales applied before the epilogue (optional)
 };
 
-// Bytes of the arrival counters at the head of a split-K fix-up workspace.
-__host__ __device__ constexpr int64_t fix_counter_bytes(int64_t tiles) { return (tiles * 8 + 255) / 256 * 256; }
 
 template <typename T>
 struct Mfma;
@@ -536,11 +535,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       // slice order (deterministic) and runs the epilogue.
       constexpr int kCoherent = 17;  // sc0 | sc1
       constexpr int TILE_B = BM * BN * 4;
-      const int tiles = a.tiles_m * a.tiles_n;
-      const int tile = tm * a.tiles_n + tn;
+      const int tile = tm * a.tiles_n + tn;  // < kWsMaxTiles (the planner's check)
       unsigned long long* cnt = (unsigned long long*)a.fix + tile;
       const __amdgpu_buffer_rsrc_t rP =
-          make_rsrc(a.fix + fix_counter_bytes(tiles) + (int64_t)tile * a.batch * TILE_B, (uint32_t)(a.batch * TILE_B));
+          make_rsrc(a.fix + kWsCounterBytes + (int64_t)tile * a.batch * TILE_B, (uint32_t)(a.batch * TILE_B));
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -555,18 +553,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       __shared__ int is_last;
       __syncthreads();
       if (threadIdx.x == 0) {
-        // first guess: the state the last call with this epoch left (a graph
-        // replay); a failed exchange returns the current value, and every
-        // later failure means another slice arrived (lock-free)
-        unsigned long long cur = a.epoch << 8, arrived = 0;
-        for (int tries = 0; tries < (1 << 16); ++tries) {
-          arrived = (cur >> 8) == a.epoch ? (cur & 255u) : 0ull;
-          if (__hip_atomic_compare_exchange_strong(cnt, &cur, (a.epoch << 8) | (arrived + 1), __ATOMIC_RELAXED,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            break;
-        }
-        is_last = arrived + 1 == (unsigned long long)a.batch;
-        if (is_last) __hip_atomic_store(cnt, a.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // every other slice of this tile has stored its partials once the
+        // count reaches batch; that slice alone touches the counter again
+        const unsigned long long before =
+            __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = before + 1 == (unsigned long long)a.batch;
+        if (is_last) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
       if (!is_last) return;

@@ -22,10 +22,6 @@
 //   * gemv_pair_ks: K > 1024 on at most 2048 rows (down projections), the
 //     same loads with K split over one workgroup's waves;
 //   * gemv_valu: M <= 8 on other long matrices, on the vector ALUs.
-#include <stdlib.h>
-
-#include <atomic>
-
 #include "hxmi_common.h"
 #include "hxmi_internal.h"
 
@@ -41,16 +37,14 @@ struct VArgs {
   int M, N, K;
   int64_t ldx, ldw, ldy;
   // K split over kg workgroups per row group (kg > 1): workspace with one
-  // arrival counter per 16-row tile, then kg fp32 partial tiles per tile;
-  // epoch tags the call so counters left by other calls count as zero
+  // 64-bit arrival counter per 16-row tile, then kg fp32 partial tiles per
+  // tile.  The counters are zero when the launch starts; the last K group of
+  // a tile resets its counter to zero, so every launch leaves them zero.
   int kg;
   char* ws;
-  unsigned long long epoch;
 };
 
 typedef float float2v __attribute__((ext_vector_type(2)));
-
-__host__ __device__ constexpr int64_t gemv_counter_bytes(int64_t tiles) { return (tiles * 8 + 255) / 256 * 256; }
 
 __device__ __forceinline__ float4v mfma16(short8v a, short8v b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a), __builtin_bit_cast(half8v, b),
@@ -163,35 +157,22 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
       // counter; the last K group adds all partials in K-group order and
       // finishes the tile.
       constexpr int kCoherent = 17;  // sc0 | sc1
-      const int tile = rg * TPB + t;
-      const int tiles = (a.N + TPB * 16 - 1) / (TPB * 16) * TPB;
+      const int tile = rg * TPB + t;  // < kWsMaxTiles (the planner's check)
       unsigned long long* cnt = (unsigned long long*)a.ws + tile;
-      float* part = (float*)(a.ws + gemv_counter_bytes(tiles)) + (int64_t)tile * a.kg * 256;
+      float* part = (float*)(a.ws + kWsCounterBytes) + (int64_t)tile * a.kg * 256;
       const __amdgpu_buffer_rsrc_t rP = make_rsrc(part, a.kg * 1024);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, sum), rP, (uint32_t)(kgi * 1024 + lane * 16), 0,
                                              kCoherent);
       wait_vmcnt0();
       unsigned long long arrived = 0;
-      if (lane == 0) {
-        // first guess: the state the last call with this epoch left (a graph
-        // replay); a failed exchange returns the current value, so a wrong
-        // guess costs one round trip and every later failure means another
-        // K group arrived (lock-free)
-        unsigned long long cur = a.epoch << 8;
-        for (int tries = 0; tries < (1 << 16); ++tries) {
-          arrived = (cur >> 8) == a.epoch ? (cur & 255u) : 0ull;
-          if (__hip_atomic_compare_exchange_strong(cnt, &cur, (a.epoch << 8) | (arrived + 1), __ATOMIC_RELAXED,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            break;
-        }
-      }
+      if (lane == 0) arrived = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       arrived = __shfl(arrived, 0, 64);
       if (arrived + 1 != (unsigned long long)a.kg) continue;
       sum = float4v{0.f, 0.f, 0.f, 0.f};
       for (int g = 0; g < a.kg; ++g)
         sum += __builtin_bit_cast(float4v,
                                   __builtin_amdgcn_raw_buffer_load_b128(rP, (uint32_t)(g * 1024 + lane * 16), 0, kCoherent));
-      if (lane == 0) __hip_atomic_store(cnt, a.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // D[n][m]: lane holds m = lane % 16, n = 4*(lane / 16) + 0..3
     const int m = lane & 15;
@@ -570,7 +551,7 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   // 448 / 512 / 576 / 640 / 1024 gave 28.0 / 26.7 / 25.3 / 31.4 / 29.1 /
   // 27.0 us: half the bytes per tile, and fewer concurrent row streams)
   int cap = I8 ? 512 : 1024;
-  if (const char* e = getenv("HXMI_GEMV_PAIR_WG")) cap = atoi(e) > 0 ? atoi(e) : cap;
+  if (const int64_t e = knob(KNOB_GEMV_PAIR_WG); e != KNOB_UNSET && e > 0) cap = e < (1 << 20) ? (int)e : (1 << 20);
   if (blocks > cap) blocks = cap;
   if constexpr (I8)
     hipLaunchKernelGGL((gemv_pair_i8<8>), dim3(blocks), dim3(256), 0, stream, v);
@@ -705,7 +686,7 @@ hipError_t launch_cfg(const VArgs& v, hipStream_t stream) {
   const int per_wave = ((v.K + kstep - 1) / kstep + KS * v.kg - 1) / (KS * v.kg);
   const int blocks = (v.N + TPB * 16 - 1) / (TPB * 16) * v.kg;
   int unr = TPB >= 4 ? 2 : (per_wave >= 12 ? (TPB == 1 ? 16 : 8) : 4);
-  if (const char* e = getenv("HXMI_GEMV_UNR")) unr = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : (TPB >= 4 ? 2 : 4));
+  if (const int64_t e = knob(KNOB_GEMV_UNR); e != KNOB_UNSET) unr = e >= 16 ? 16 : (e >= 8 ? 8 : (TPB >= 4 ? 2 : 4));
   if constexpr (TPB < 4) {
     if (unr == 16 && TPB == 1) {
       hipLaunchKernelGGL((gemv_mfma<1, KS, I8, 16>), dim3(blocks), dim3(KS * 64), 0, stream, v);
@@ -764,8 +745,9 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   const int64_t nsteps = (p.K + kstep - 1) / kstep;
   while (g.ks > 4 && nsteps / g.ks < 2) g.ks /= 2;
   // tuning overrides (launch shape only; every shape computes the same sums)
-  if (const char* e = getenv("HXMI_GEMV_TPB")) g.tpb = atoi(e) == 4 ? 4 : (atoi(e) == 2 ? 2 : 1);
-  if (const char* e = getenv("HXMI_GEMV_KS")) g.ks = atoi(e) >= 16 ? 16 : (atoi(e) >= 8 ? 8 : 4);
+  const int64_t ks_knob = knob(KNOB_GEMV_KS);
+  if (const int64_t e = knob(KNOB_GEMV_TPB); e != KNOB_UNSET) g.tpb = e == 4 ? 4 : (e == 2 ? 2 : 1);
+  if (ks_knob != KNOB_UNSET) g.ks = ks_knob >= 16 ? 16 : (ks_knob >= 8 ? 8 : 4);
   // Measured on the Qwen2.5-0.5B shapes (graph replays, weights rotating
   // past the Infinity Cache):
   //  * whole-line MFMA kernel (K <= 1024): long weight matrices -- lm_head
@@ -796,15 +778,15 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
   if (g.pair_ks) {
     const int64_t nwin = (p.K + (p.w_int8 ? 127 : 63)) / (p.w_int8 ? 128 : 64);
     g.ks = (p.M > 4 && nwin >= 64) ? 16 : 8;
-    if (const char* e = getenv("HXMI_GEMV_KS")) g.ks = atoi(e) >= 16 ? 16 : 8;
+    if (ks_knob != KNOB_UNSET) g.ks = ks_knob >= 16 ? 16 : 8;
   }
   g.valu = !g.pair && !g.pair_ks && fits && p.M <= 8 &&
            (p.w_int8 ? (p.N >= 32768 && p.M <= 4) : ((p.N >= 32768) || (p.M == 1 && p.N >= 4096)));
-  if (const char* e = getenv("HXMI_GEMV_PATH")) {
-    g.valu = (e[0] == 'v') && fits;
-    g.pair = (e[0] == 'p') && xfits;
-    g.pair_ks = (e[0] == 'k');
-    if (g.pair_ks && !getenv("HXMI_GEMV_KS")) g.ks = 8;
+  if (const int64_t e = knob(KNOB_GEMV_PATH); e != KNOB_UNSET) {
+    g.valu = e == GEMV_PATH_VALU && fits;
+    g.pair = e == GEMV_PATH_PAIR && xfits;
+    g.pair_ks = e == GEMV_PATH_PAIR_KS;
+    if (g.pair_ks && ks_knob == KNOB_UNSET) g.ks = 8;
   }
   if (g.valu || g.pair || g.pair_ks) return g;
   // few row groups, each streaming a long K (e.g. a down projection
@@ -821,7 +803,7 @@ static GemvPlan gemv_plan(const GemvProblem& p) {
     while (kg > 1 && nsteps / kg < 2 * g.ks) --kg;
     g.kg = kg;
   }
-  if (const char* e = getenv("HXMI_GEMV_KG")) g.kg = atoi(e) < 1 ? 1 : (atoi(e) > 16 ? 16 : atoi(e));
+  if (const int64_t e = knob(KNOB_GEMV_KG); e != KNOB_UNSET) g.kg = e < 1 ? 1 : (e > 16 ? 16 : (int)e);
   return g;
 }
 
@@ -829,7 +811,7 @@ int64_t gemv_workspace_bytes(const GemvProblem& p) {
   const GemvPlan g = gemv_plan(p);
   if (g.valu || g.pair || g.pair_ks || g.kg <= 1) return 0;
   const int64_t tiles = (p.N + g.tpb * 16 - 1) / (g.tpb * 16) * g.tpb;  // 16-row tiles of whole row groups
-  return gemv_counter_bytes(tiles) + tiles * g.kg * 1024;
+  return tiles > kWsMaxTiles ? 0 : kWsCounterBytes + tiles * g.kg * 1024;
 }
 
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
@@ -848,16 +830,14 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.ldy = p.ldy;
   v.kg = 1;
   v.ws = nullptr;
-  v.epoch = 0;
   const GemvPlan g = gemv_plan(p);
   if (g.valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
   if (g.pair) return p.w_int8 ? launch_pair<true>(v, stream) : launch_pair<false>(v, stream);
   if (g.pair_ks) return p.w_int8 ? launch_pair_ks<true>(v, g.ks, stream) : launch_pair_ks<false>(v, g.ks, stream);
-  if (g.kg > 1 && p.ws && p.ws_bytes >= gemv_workspace_bytes(p) && ((uintptr_t)p.ws % 256) == 0) {
-    static std::atomic<unsigned long long> calls{1};
+  const int64_t need = g.kg > 1 ? gemv_workspace_bytes(p) : 0;
+  if (need > 0 && p.ws && p.ws_bytes >= need && ((uintptr_t)p.ws % 256) == 0) {
     v.kg = g.kg;
     v.ws = (char*)p.ws;
-    v.epoch = calls.fetch_add(1) & ((1ull << 56) - 1);
   }
   return p.w_int8 ? launch_sel<true>(g.tpb, g.ks, v, stream) : launch_sel<false>(g.tpb, g.ks, v, stream);
 }

@@ -19,6 +19,38 @@ enum Epilogue {
 
 enum OutType { OUT_SAME = 0, OUT_F32 = 1 };
 
+// Layout of a split-K workspace (GEMM and GEMV alike): a fixed region of
+// 64-bit arrival counters at the head, one per output tile of the call,
+// then the fp32 partial tiles.  Fixing the counter region for every shape
+// lets one zero-filled workspace serve calls of different shapes: a call
+// writes partials only past the region and leaves its counters zero.
+// A problem whose split would need more tiles than counters runs unsplit.
+constexpr int64_t kWsCounterBytes = 16384;
+constexpr int64_t kWsMaxTiles = kWsCounterBytes / 8;
+
+// Launch-shape tuning knobs (tuning.hip): the environment value HXMI_<NAME>
+// read once at load, overridden per thread by hxmi_set_tuning.
+enum Knob {
+  KNOB_GEMM_TILE = 0,  // forced GEMM TileId
+  KNOB_GROUP_M,        // tile-rows per raster group
+  KNOB_SPLITK,         // forced K slice count
+  KNOB_W8_TILE,        // forced tile of the int8-weight GEMM
+  KNOB_GEMV_PATH,      // GemvPath
+  KNOB_GEMV_TPB,       // 16-row tiles per workgroup of the MFMA GEMV
+  KNOB_GEMV_KS,        // waves splitting K inside a GEMV workgroup
+  KNOB_GEMV_KG,        // workgroups splitting K per GEMV row group
+  KNOB_GEMV_UNR,       // K-steps in flight per GEMV wave
+  KNOB_GEMV_PAIR_WG,   // workgroup cap of the whole-line GEMV
+  KNOB_COUNT
+};
+enum GemvPath { GEMV_PATH_MFMA = 0, GEMV_PATH_VALU = 1, GEMV_PATH_PAIR = 2, GEMV_PATH_PAIR_KS = 3 };
+constexpr int64_t KNOB_UNSET = INT64_MIN;
+int64_t knob(Knob k);  // KNOB_UNSET: the library's own choice
+int knob_index(const char* name);
+// Sets this thread's override of knob k (value < 0 clears it); returns the
+// previous override, -1 if there was none.
+int64_t set_knob_override(int k, int64_t value);
+
 // One (optionally batched) GEMM  C[b] = epilogue(alpha * A[b] . op(B[b])).
 // A is [M,K] row-major with leading dimension lda.  B is [K,N] (b_nt = 0) or
 // [N,K] (b_nt = 1).  For EPI_SILU_MUL, N counts the packed gate/up columns of
@@ -133,5 +165,9 @@ struct AttnProblem {
 };
 
 hipError_t launch_attention(const AttnProblem& p, hipStream_t stream);
+
+// Region profiling: record `slot` of `records` (3 words each) = {id, wall
+// clock low word, high word}, taken when the marker runs on `stream`.
+hipError_t launch_lwp_mark(uint32_t* records, int64_t slot, uint32_t id, hipStream_t stream);
 
 }  // namespace hxmi

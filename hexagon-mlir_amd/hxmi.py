@@ -7,6 +7,8 @@ raises.
 """
 from __future__ import annotations
 
+import collections
+import contextlib
 import ctypes
 import pathlib
 from typing import Optional
@@ -32,6 +34,7 @@ _I = ctypes.c_int
 SIGNATURES = {
     "hxmi_last_error": ([], ctypes.c_char_p),
     "hxmi_version": ([], _I),
+    "hxmi_set_tuning": ([ctypes.c_char_p, _I64, ctypes.POINTER(_I64)], _I),
     "hxmi_gemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P], _I),
     "hxmi_gemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P], _I),
     "hxmi_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
@@ -49,6 +52,8 @@ SIGNATURES = {
     "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_quantize_int8_rows_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_lwp_record": ([_P, _I64, ctypes.c_uint32, _P], _I),
+    "hxmi_lwp_clock_hz": ([], _I64),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
 }
 
@@ -83,6 +88,37 @@ def _check(rc: int) -> None:
     if rc != 0:
         msg = load_library().hxmi_last_error().decode(errors="replace")
         raise HxmiError(f"hxmi error {rc}: {msg}")
+
+
+TUNING_KNOBS = ("gemm_tile", "group_m", "splitk", "w8_tile", "gemv_path", "gemv_tpb", "gemv_ks", "gemv_kg",
+                "gemv_unr", "gemv_pair_wg")
+
+
+def set_tuning(name: str, value) -> Optional[int]:
+    """Set (or with None clear) this thread's override of a launch-shape knob;
+    returns the previous override (None if there was none).  gemv_path also
+    takes a kernel name, read by its first letter as HXMI_GEMV_PATH is:
+    "valu", "pair", "ksplit" (whole-line pairs, K split), else the 16-row
+    MFMA kernel."""
+    if isinstance(value, str):
+        value = {"v": 1, "p": 2, "k": 3}.get(value[:1], 0) if name == "gemv_path" else int(value)
+    prev = ctypes.c_int64(-1)
+    _check(load_library().hxmi_set_tuning(name.encode(), -1 if value is None else int(value), ctypes.byref(prev)))
+    return None if prev.value < 0 else prev.value
+
+
+@contextlib.contextmanager
+def tuning(**knobs):
+    """Launch-shape overrides for the calls made inside the block on this
+    thread, restored afterwards, e.g. ``with tuning(gemm_tile=3): ...``."""
+    saved = {}
+    try:
+        for name, value in knobs.items():
+            saved[name] = set_tuning(name, value)
+        yield
+    finally:
+        for name, prev in saved.items():
+            set_tuning(name, prev)
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -129,14 +165,31 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+_WS_CACHE: "collections.OrderedDict[tuple[int, int], torch.Tensor]" = collections.OrderedDict()
+_WS_KEEP = 16  # workspaces kept (one per device and stream, least recently used dropped)
+
+
 def _workspace(nbytes: int, device: torch.device) -> Optional[torch.Tensor]:
-    """Split-K scratch from torch's caching allocator.  The block returns to
-    the allocator when the tensor dies after the launch; the allocator only
-    hands it out again in the order of the stream it was allocated on, so the
-    kernels that use it finish first and concurrent streams never share it."""
+    """Split-K scratch for the current stream of `device`.  The C ABI wants the
+    arrival counters at its head zero when a call starts and leaves them zero
+    afterwards, so one zero-filled buffer per (device, stream) serves every
+    call on that stream; it is replaced by a larger zero-filled one when a call
+    needs more.  Allocated on that stream, a dropped buffer is handed out
+    again by torch's caching allocator only in that stream's order, after the
+    kernels that used it; calls on different streams never share one."""
     if nbytes <= 0:
         return None
-    return torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _raw_stream(device.index) if _raw_stream is not None else torch.cuda.current_stream(device).cuda_stream)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        # torch.zeros clears with a fill kernel, which is also safe inside graph capture
+        ws = torch.zeros((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+        _WS_CACHE[key] = ws
+    _WS_CACHE.move_to_end(key)
+    while len(_WS_CACHE) > _WS_KEEP:
+        _WS_CACHE.popitem(last=False)
+    return ws
 
 
 def gemm(
@@ -235,10 +288,11 @@ def bgemm(
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
-           epilogue: Optional[str] = None) -> torch.Tensor:
+           epilogue: Optional[str] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """nn.Linear forward, y = x @ w.T (+ bias), with an optional fused activation.
 
     epilogue: None, "gelu_tanh" or "silu_mul" (w then packed by pack_gate_up).
+    out: optional 2-D destination [rows of x, output features].
     """
     if epilogue is None:
         epi = "bias" if bias is not None else None
@@ -252,8 +306,8 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None
         raise HxmiError(f"unknown activation {epilogue!r}")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
-    y = gemm(x2, w, b_layout="nt", epilogue=epi, bias=bias)
-    return y.reshape(*lead, y.shape[-1])
+    y = gemm(x2, w, b_layout="nt", epilogue=epi, bias=bias, out=out)
+    return y if out is not None else y.reshape(*lead, y.shape[-1])
 
 
 def fold_rms_weight(w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
@@ -414,7 +468,8 @@ def softmax(x: torch.Tensor, scale: float = 1.0, out: Optional[torch.Tensor] = N
     return out2.reshape(*lead, cols)
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """SDPA as the reference lowers it (LowerTmTensor.cpp:91-250): softmax(scale * Q.K^T) . V over
     q [..., S, D], k and v [..., S_kv, D].  fp16 with D in {64, 128} runs the fused kernel
     (hxmi_attention_f16); other cases run the same three steps as bmm(Q, K^T) -> softmax -> bmm(P, V)."""
@@ -431,16 +486,29 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional
         _require_gpu(q3, k3, v3)
         q3, k3, v3 = (t if t.stride(-1) == 1 and t.stride(1) % 8 == 0 and t.stride(0) % 8 == 0
                       and t.data_ptr() % 16 == 0 else t.contiguous() for t in (q3, k3, v3))
-        o = torch.empty((q3.shape[0], S, D), dtype=q.dtype, device=q.device)
+        if out is None:
+            o = torch.empty((q3.shape[0], S, D), dtype=q.dtype, device=q.device)
+        else:
+            if out.shape != (*lead, S, D) or out.dtype != q.dtype:
+                raise HxmiError(f"out must be {q.dtype} {(*lead, S, D)}")
+            o = out.reshape(-1, S, D)
+            if o.data_ptr() != out.data_ptr() or o.stride(-1) != 1 or o.data_ptr() % 8 or o.stride(1) % 4 \
+                    or o.stride(0) % 4:
+                raise HxmiError("out must be a view with unit last stride and 8-byte aligned rows")
+        _require_gpu(o)
         ldq, bq = _batched(q3, "q")
         ldk, bk = _batched(k3, "k")
         ldv, bv = _batched(v3, "v")
+        ldo, bo = _batched(o, "out")
         _check(load_library().hxmi_attention_f16(q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), o.data_ptr(),
-                                                 q3.shape[0], S, k3.shape[1], D, ldq, ldk, ldv, D, bq, bk, bv,
-                                                 S * D, float(scale), _stream(q)))
-        return o.reshape(*lead, S, D)
+                                                 q3.shape[0], S, k3.shape[1], D, ldq, ldk, ldv, ldo, bq, bk, bv,
+                                                 bo, float(scale), _stream(q)))
+        return out if out is not None else o.reshape(*lead, S, D)
     s = bgemm(q3, k3, b_layout="nt", alpha=scale)
     p = softmax(s)
+    if out is not None:
+        bgemm(p, v3, b_layout="nn", out=out.view(-1, S, v.shape[-1]))
+        return out
     o = bgemm(p, v3, b_layout="nn")
     return o.reshape(*lead, S, v.shape[-1])
 

@@ -41,6 +41,9 @@ typedef uint16_t hxmi_f16_t;
 #define HXMI_ERR_UNSUPPORTED 2
 #define HXMI_ERR_HIP 3
 
+/* Bytes of arrival counters at the head of every split-K workspace. */
+#define HXMI_WORKSPACE_COUNTER_BYTES 16384
+
 /* GEMM epilogues, applied to alpha * (A . op(B)) in fp32 before the store. */
 #define HXMI_EPI_NONE 0
 #define HXMI_EPI_BIAS 1           /* + bias[n]                                  */
@@ -53,6 +56,22 @@ const char* hxmi_last_error(void);
 
 /* Library version, major * 10000 + minor * 100 + patch. */
 int hxmi_version(void);
+
+/*
+ * Launch-shape tuning override for the calls this thread makes afterwards
+ * (value < 0 removes it).  Knobs: "gemm_tile" (forced GEMM tile id),
+ * "group_m", "splitk", "w8_tile", "gemv_path" (0 16-row MFMA, 1 vector-ALU
+ * rows, 2 whole-line pairs, 3 whole-line pairs with K split), "gemv_tpb",
+ * "gemv_ks", "gemv_kg", "gemv_unr", "gemv_pair_wg".  A knob without a thread
+ * override takes the value of the environment variable HXMI_<NAME> read once
+ * when the library loaded, else the library's own choice.  Knobs change how a
+ * result is computed (tile, K split, kernel), not what it is.  *previous
+ * (optional) receives the thread's previous override, -1 if none, so a caller
+ * can restore it.
+ * Replaces: the compile options that steer the reference's tiling for one
+ * compilation (tileSizes, hexagon_options.py:17-88), scoped here to a thread.
+ */
+int hxmi_set_tuning(const char* name, int64_t value, int64_t* previous);
 
 /*
  * C[M,N] = epilogue(alpha * A[M,K] . op(B)), fp32 accumulation, fp16 output.
@@ -68,7 +87,15 @@ int hxmi_version(void);
  * the last slice to finish an output tile adds them in slice order and
  * applies the epilogue (one launch).  It needs hxmi_gemm_workspace_bytes()
  * bytes.  NULL / 0 (or a smaller or misaligned buffer) runs the GEMM
- * unsplit.  Two calls must not share a workspace concurrently.
+ * unsplit.  Workspace contract (every entry point that takes one): the
+ * first HXMI_WORKSPACE_COUNTER_BYTES bytes hold per-tile arrival counters,
+ * which must be zero when a call that uses the workspace starts; partial
+ * tiles go after them.  Zero the whole buffer once after allocating it:
+ * every call leaves its counters zero again and writes nothing else into
+ * that region, so one buffer serves later calls of any shape (and graph
+ * replays) on the same stream without being cleared.  A counter region
+ * holding anything else gives wrong results.  Two calls must not use one
+ * workspace concurrently.
  * Replaces: the linalg.matmul / matmul_transpose_b lowering scheduled by
  * ScheduleMatmulForHVXPass.cpp:69-195 and tiled by VTCMTiling.cpp:231-266
  * (with HexmemCpyToDMA.cpp:120-271 DMA staging), plus the elementwise
@@ -109,7 +136,8 @@ int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int
  * (256-byte aligned).  With few output rows and a long K (a down
  * projection) the GEMV splits K over workgroups, which combine their fp32
  * partial tiles there; it needs hxmi_gemv_workspace_bytes() bytes.  NULL / 0
- * runs unsplit.  Two calls must not share a workspace concurrently.
+ * runs unsplit.  Same workspace contract as hxmi_gemm_f16 (zeroed once after
+ * allocation, left zeroed by every call, one call at a time).
  * Replaces: the M = 1 matmul_transpose_b that the reference sends through
  * the same generic HVX schedule (TilingPass.cpp:108-251); it has no GEMV.
  */
@@ -222,6 +250,26 @@ int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, in
 int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q, int64_t s_kv,
                        int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t stride_q,
                        int64_t stride_k, int64_t stride_v, int64_t stride_o, float scale, void* stream);
+
+/*
+ * Region profiling hook: enqueues on `stream` a one-wave marker that, when it
+ * runs (after every kernel enqueued before it on that stream has finished),
+ * writes record `slot` of `records` -- three uint32 words {id, t low word,
+ * t high word}, t the GPU's constant-rate wall clock -- so a begin and an end
+ * record with the same id bracket the kernels enqueued between them.  The
+ * buffer is device memory of at least 3 * (slot + 1) words, owned by the
+ * caller; slots are the caller's to assign (no two in-flight records may
+ * share one).  Written out as {"entries": [{"id": id, "cyc": t}, ...]} in
+ * record order, the records are what the reference's region tooling reads.
+ * Replaces: the LWP instrumentation hooks and record buffer
+ * (test/utils/dsp/include/prof_utils.cc:37-60, bin/runtime/profiler/
+ * lwp_handler.S), whose JSON test/python/process_lwp.py:20-60 folds.
+ */
+int hxmi_lwp_record(uint32_t* records, int64_t slot, uint32_t id, void* stream);
+
+/* Ticks per second of the clock hxmi_lwp_record reads, for the current
+ * device (0 if it cannot be queried). */
+int64_t hxmi_lwp_clock_hz(void);
 
 /*
  * HexKL-compatible matmul: outM[n_row, n_col] (fp32) = inAct[n_row, n_inner]

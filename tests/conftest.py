@@ -1,4 +1,3 @@
-import os
 import pathlib
 import sys
 
@@ -32,18 +31,22 @@ def dev():
 
 
 @pytest.fixture
-def force_tile():
-    """Force the GEMM tile shape for the duration of a test (HXMI_GEMM_TILE)."""
-    old = os.environ.get("HXMI_GEMM_TILE")
+def knobs(pkg):
+    """Launch-shape overrides (hxmi_set_tuning) for the duration of a test:
+    knobs(gemm_tile=3, splitk=4, ...); None clears one."""
+    saved = {}
 
-    def _set(t):
-        if t is None:
-            os.environ.pop("HXMI_GEMM_TILE", None)
-        else:
-            os.environ["HXMI_GEMM_TILE"] = str(t)
+    def _set(**kw):
+        for name, value in kw.items():
+            prev = pkg.set_tuning(name, value)
+            saved.setdefault(name, prev)
 
     yield _set
-    if old is None:
-        os.environ.pop("HXMI_GEMM_TILE", None)
-    else:
-        os.environ["HXMI_GEMM_TILE"] = old
+    for name, prev in saved.items():
+        pkg.set_tuning(name, prev)
+
+
+@pytest.fixture
+def force_tile(knobs):
+    """Force the GEMM tile shape (TileId) for the duration of a test."""
+    return lambda t: knobs(gemm_tile=t)

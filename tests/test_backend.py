@@ -292,3 +292,59 @@ def test_etm_is_not_available(backend, tmp_path):
     with pytest.raises(NotImplementedError):
         backend.TorchMLIRHexagonLauncher(torch.device("cpu")).run_torch_mlir(
             "missing.pt2", [], "f", str(tmp_path), enable_etm=True)
+
+
+# ---- LWP region timing files --------------------------------------------------------
+
+
+def fold_lwp(entries):
+    """The pairing rule of the reference's region tooling
+    (test/python/process_lwp.py:20-60), restated: a record whose id is on top
+    of the stack of open regions closes it, any other record opens a region
+    (an id may not reopen while open); returns {id: (total, count, parent)}."""
+    stack, summary = [], {}
+    for e in entries:
+        rid, cyc = e["id"], e["cyc"]
+        if stack and stack[-1][0] == rid:
+            _, start, parent = stack.pop()
+            tot, cnt, par = summary.get(rid, (0, 0, None))
+            summary[rid] = (tot + cyc - start, cnt + 1, par if par is not None else parent)
+        else:
+            assert rid not in [s[0] for s in stack], f"region {rid} reopened while open"
+            stack.append((rid, cyc, stack[-1][0] if stack else None))
+    assert not stack, f"regions left open: {stack}"
+    return summary
+
+
+def test_lwp_files_follow_the_reference_layout(backend):
+    from hexagon_mlir_amd.backend import lwp
+
+    entries = [{"id": 0, "cyc": 100}, {"id": 1, "cyc": 110}, {"id": 1, "cyc": 150}, {"id": 2, "cyc": 150},
+               {"id": 2, "cyc": 400}, {"id": 0, "cyc": 401}]
+    text = lwp.lwp_json(entries, 100_000_000)
+    d = json_loads(text)
+    assert d["entries"] == entries and d["cyc_hz"] == 100_000_000
+    # prof_utils.cc:37-60 writes one {"id", "cyc"} object per record, in order
+    assert re.search(r'"entries": \[\n    \{\n      "id": 0,\n      "cyc": 100\n    \},', text)
+    s = fold_lwp(d["entries"])
+    assert s == {1: (40, 1, 0), 2: (250, 1, 0), 0: (301, 1, None)}
+    dump = lwp.infodump_lines([(0, [0], ["func"]), (1, [3], ["linear_1: hx_linear"]), (2, [5, 6], ["a", "b"])])
+    # the line format process_lwp.py:63-88 reads
+    pat = re.compile(r"Location ([\d,\s]+) corresponds to ID (\d+)")
+    parsed = {}
+    for line in dump.strip().split("\n"):
+        loc, ops = line.split(" | Collected ops:", 1)
+        m = pat.search(loc)
+        parsed[int(m.group(2))] = ([int(v) for v in m.group(1).split(",")], [o.strip() for o in ops.split(",")])
+    assert parsed == {0: ([0], ["func"]), 1: ([3], ["linear_1: hx_linear"]), 2: ([5, 6], ["a", "b"])}
+
+
+def test_lwp_pairing_rejects_interleaved_regions():
+    with pytest.raises(AssertionError, match="reopened"):
+        fold_lwp([{"id": 1, "cyc": 0}, {"id": 2, "cyc": 1}, {"id": 1, "cyc": 2}])
+
+
+def json_loads(text):
+    import json
+
+    return json.loads(text)

@@ -143,3 +143,42 @@ def test_quantizer_rejects_invalid_arguments(pkg, args, msg):
     assert lib.hxmi_quantize_int8_rows_f16(*args) == 1
     assert msg in lib.hxmi_last_error().decode()
     assert lib.hxmi_quantize_int8_rows_f16(None, None, None, 0, 8, 8, 8, None) == 0
+
+
+def test_tuning_overrides_are_per_thread_and_restorable(pkg):
+    """hxmi_set_tuning: per-thread launch-shape overrides, each call returning
+    the previous one so a scope can restore it (no GPU work involved)."""
+    import threading
+
+    assert pkg.set_tuning("gemm_tile", 3) is None
+    assert pkg.set_tuning("gemm_tile", 5) == 3
+    other = []
+    t = threading.Thread(target=lambda: other.append(pkg.set_tuning("gemm_tile", None)))
+    t.start()
+    t.join()
+    assert other == [None]  # another thread does not see this thread's override
+    assert pkg.set_tuning("gemm_tile", None) == 5
+    with pkg.tuning(splitk=4, gemv_path="ksplit"):
+        assert pkg.set_tuning("splitk", 4) == 4
+        assert pkg.set_tuning("gemv_path", 3) == 3
+    assert pkg.set_tuning("splitk", None) is None and pkg.set_tuning("gemv_path", None) is None
+    with pytest.raises(pkg.HxmiError, match="unknown knob"):
+        pkg.set_tuning("no_such_knob", 1)
+
+
+def test_plan_tile_applies_to_its_own_runs_only(pkg):
+    from hexagon_mlir_amd.backend.graph import Plan
+
+    seen = []
+
+    class Probe:
+        def __call__(self, *args):
+            prev = pkg.set_tuning("gemm_tile", None)
+            seen.append(prev)
+            pkg.set_tuning("gemm_tile", prev)
+            return args
+
+    Plan(module=Probe(), gemm_tile=6)(1)
+    Plan(module=Probe())(1)
+    assert seen == [6, None]
+    assert pkg.set_tuning("gemm_tile", None) is None

@@ -172,14 +172,8 @@ def test_bgemm_vit_attention_products(pkg, dev):
 
 
 @pytest.fixture
-def force_splits(monkeypatch):
-    def _set(s):
-        if s is None:
-            monkeypatch.delenv("HXMI_SPLITK", raising=False)
-        else:
-            monkeypatch.setenv("HXMI_SPLITK", str(s))
-
-    return _set
+def force_splits(knobs):
+    return lambda s: knobs(splitk=s)
 
 
 @pytest.mark.parametrize("layout", ["nn", "nt"])
@@ -239,7 +233,7 @@ def test_gemm_split_k_deterministic_graph_replays(pkg, dev, force_splits):
     shapes = [(512, 2048, 5632), (200, 640, 4096)]
     nbytes = max(lib.hxmi_gemm_workspace_bytes(M, N, K, 1, 0) for M, N, K in shapes)
     assert nbytes > 0
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)  # counters zero before first use
     ops = []
     for i, (M, N, K) in enumerate(shapes):
         x = normal((M, K), 44 + i).to(dev)
@@ -277,6 +271,33 @@ def test_gemm_split_k_deterministic_graph_replays(pkg, dev, force_splits):
         call(ops[1], None)  # another shape on the same workspace between replays
         torch.cuda.synchronize()
         assert torch.equal(ops[1][2], eager[1])
+
+
+def test_gemm_split_k_workspace_counters_return_to_zero(pkg, dev, force_splits):
+    """The workspace protocol: arrival counters zero when a call starts, zero
+    again when it ends; whatever an earlier user left in the partial-tile
+    area (here int64 words that look like tagged counts) does not matter."""
+    force_splits(3)
+    lib = pkg.load_library()
+    M, N, K = 200, 640, 4096
+    nbytes = lib.hxmi_gemm_workspace_bytes(M, N, K, 1, 0)
+    cwords = 16384 // 8  # HXMI_WORKSPACE_COUNTER_BYTES of 64-bit counters
+    assert nbytes > cwords * 8
+    ws = torch.zeros(nbytes // 8, dtype=torch.int64, device=dev)
+    ws[cwords:] = (torch.arange(nbytes // 8 - cwords, device=dev) % 7) | (1 << 8)
+    x, w = normal((M, K), 60).to(dev), normal((N, K), 61, 0.02).to(dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    exp = ref.linear(x.cpu().numpy(), w.cpu().numpy())
+    first = None
+    for _ in range(3):
+        rc = lib.hxmi_gemm_f16(x.data_ptr(), w.data_ptr(), y.data_ptr(), None, M, N, K, K, K, N, 1, 0, 1.0,
+                               ws.data_ptr(), nbytes, None)
+        assert rc == 0, lib.hxmi_last_error()
+        torch.cuda.synchronize()
+        assert int(ws[:cwords].abs().sum()) == 0
+        assert ref.max_rel_err(np32(y.cpu()), exp) <= TOL
+        first = y.clone() if first is None else first
+        assert torch.equal(y, first)
 
 
 def test_gemm_split_k_default_down_projection(pkg, dev):

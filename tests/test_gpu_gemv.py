@@ -67,13 +67,13 @@ def test_w8a16_qwen_shapes(pkg, dev, M, K, N):
 
 
 @pytest.fixture
-def gemv_path(monkeypatch):
+def gemv_path(knobs):
     """Force the decode kernel: "mfma" (16-row MFMA tiles, K split over
     waves), "valu" (row streaming) or "pair" (8-row tiles, whole-line
     loads, each row read as two MFMA rows, K <= 1024)."""
 
     def force(path):
-        monkeypatch.setenv("HXMI_GEMV_PATH", path)
+        knobs(gemv_path=path)
 
     return force
 
@@ -155,12 +155,11 @@ def test_w8a16_bias_and_scale_linearity(pkg, dev):
 
 
 @pytest.fixture
-def gemv_kgroups(monkeypatch):
+def gemv_kgroups(knobs):
     """Force the number of workgroups that split K per row group (1 = unsplit)."""
 
     def force(kg):
-        monkeypatch.setenv("HXMI_GEMV_PATH", "mfma")
-        monkeypatch.setenv("HXMI_GEMV_KG", str(kg))
+        knobs(gemv_path="mfma", gemv_kg=kg)
 
     return force
 
@@ -216,7 +215,7 @@ def test_gemv_long_k_splits_by_default(pkg, dev):
     assert lib.hxmi_gemv_workspace_bytes(1, N, K) > 0
     assert lib.hxmi_gemv_workspace_bytes(1, 4864, 896) == 0
     nbytes = max(lib.hxmi_gemv_workspace_bytes(m, N, K) for m in (1, 16))
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)  # counters zero before first use
     w = normal((N, K), 51, 0.05).to(dev)
     outs = []
     for M in (1, 16, 1, 16, 1):
@@ -236,7 +235,7 @@ def test_gemv_k_groups_graph_replays(pkg, dev):
     M, N, K = 1, 2560, 8192
     lib = pkg.load_library()
     nbytes = lib.hxmi_gemv_workspace_bytes(M, N, K)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)  # counters zero before first use
     x = normal((M, K), 61).to(dev)
     w = normal((N, K), 62, 0.05).to(dev)
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
@@ -279,6 +278,39 @@ def test_gemv_pair(pkg, dev, gemv_path, M, N, K):
     assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
 
 
+@pytest.mark.parametrize("M", [7, 16])
+@pytest.mark.parametrize("wg", [8, 3])
+def test_gemv_pair_many_tiles_per_wave(pkg, dev, gemv_path, knobs, M, wg):
+    """With few workgroups every wave walks many 8-row tiles: at M > 4 the
+    first 6 tiles' outputs are held back until the wave's last tile and the
+    later ones are stored as they finish; both halves must land."""
+    gemv_path("pair")
+    knobs(gemv_pair_wg=wg)
+    N, K = 8192 + 40, 896
+    x = normal((M, K), 74 + M)
+    w = normal((N, K), 75, 0.05)
+    b = normal((N,), 76)
+    y = pkg.gemv(x.to(dev), w.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_gemv_pair_strided_output_keeps_padding(pkg, dev, gemv_path, M):
+    """fp16 whole-line kernel writing into a wider row-major buffer: the
+    result lands in the first N columns and the padding is untouched."""
+    gemv_path("pair")
+    N, K, ldy = 8192 + 24, 640, 8192 + 64
+    x = normal((M, K), 77 + M)
+    w = normal((N, K), 78, 0.05)
+    buf = torch.full((M, ldy), -7.0, dtype=torch.float16, device=dev)
+    pkg.gemv(x.to(dev), w.to(dev), out=buf[:, :N])
+    torch.cuda.synchronize()
+    got = buf.cpu()
+    assert ref.max_rel_err(np32(got[:, :N]), ref.linear(x.numpy(), w.numpy())) <= TOL
+    assert torch.all(got[:, N:] == -7.0)
+
+
 @pytest.mark.parametrize("M", [1, 16])
 @pytest.mark.parametrize("N,K", [(2056, 1024), (24, 16), (33000, 896), (1000, 144)])
 def test_w8a16_pair(pkg, dev, gemv_path, M, N, K):
@@ -303,14 +335,37 @@ def test_gemv_valu_two_row_blocks(pkg, dev, gemv_path, M, N, K):
     assert ref.max_rel_err(np32(y.cpu()), ref.linear(x.numpy(), w.numpy())) <= TOL
 
 
+def test_gemv_k_groups_workspace_counters_return_to_zero(pkg, dev, gemv_kgroups):
+    """K groups meet on per-tile counters at the workspace's head: zero when a
+    call starts, zero again when it ends, whatever the partial area holds."""
+    gemv_kgroups(3)
+    lib = pkg.load_library()
+    M, N, K = 4, 896, 4864
+    nbytes = lib.hxmi_gemv_workspace_bytes(M, N, K)
+    cwords = 16384 // 8  # HXMI_WORKSPACE_COUNTER_BYTES of 64-bit counters
+    assert nbytes > cwords * 8
+    ws = torch.zeros(nbytes // 8, dtype=torch.int64, device=dev)
+    ws[cwords:] = (torch.arange(nbytes // 8 - cwords, device=dev) % 5) | (1 << 8)
+    x, w = normal((M, K), 70).to(dev), normal((N, K), 71, 0.05).to(dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    exp = ref.linear(x.cpu().numpy(), w.cpu().numpy())
+    for _ in range(3):
+        rc = lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), M, N, K, K, K, N, ws.data_ptr(),
+                               nbytes, None)
+        assert rc == 0, lib.hxmi_last_error()
+        torch.cuda.synchronize()
+        assert int(ws[:cwords].abs().sum()) == 0
+        assert ref.max_rel_err(np32(y.cpu()), exp) <= TOL
+
+
 @pytest.mark.parametrize("ks", ["8", "16"])
 @pytest.mark.parametrize("M", [1, 5, 16])
 @pytest.mark.parametrize("N,K", [(896, 4864), (2048, 5632), (1004, 2056), (40, 8), (300, 1288)])
-def test_gemv_pair_ksplit(pkg, dev, gemv_path, monkeypatch, ks, M, N, K):
+def test_gemv_pair_ksplit(pkg, dev, gemv_path, knobs, ks, M, N, K):
     # whole-line loads with K split over the workgroup's waves: down
     # projections, ragged windows and 8-row tiles, waves left without K
     gemv_path("ksplit")
-    monkeypatch.setenv("HXMI_GEMV_KS", ks)
+    knobs(gemv_ks=int(ks))
     x = normal((M, K), 91 + M)
     w = normal((N, K), 92, 0.05)
     b = normal((N,), 93)
@@ -322,9 +377,9 @@ def test_gemv_pair_ksplit(pkg, dev, gemv_path, monkeypatch, ks, M, N, K):
 @pytest.mark.parametrize("ks", ["8", "16"])
 @pytest.mark.parametrize("M", [1, 16])
 @pytest.mark.parametrize("N,K", [(896, 4864), (1000, 2064), (24, 16)])
-def test_w8a16_pair_ksplit(pkg, dev, gemv_path, monkeypatch, ks, M, N, K):
+def test_w8a16_pair_ksplit(pkg, dev, gemv_path, knobs, ks, M, N, K):
     gemv_path("ksplit")
-    monkeypatch.setenv("HXMI_GEMV_KS", ks)
+    knobs(gemv_ks=int(ks))
     x = normal((M, K), 95 + M)
     q, s = int8_weights(N, K, 96)
     b = normal((N,), 97)

@@ -1,4 +1,5 @@
 """GPU end-to-end through the reference-compatible launcher."""
+import json
 import re
 
 import numpy as np
@@ -8,7 +9,7 @@ import torch.nn as nn
 
 from gpu_util import TOL, normal, np32, uniform
 from oracle import hot_path as ref
-from test_backend import Block, QKVIn, block_inputs
+from test_backend import Block, QKVIn, block_inputs, fold_lwp
 
 pytestmark = pytest.mark.gpu
 
@@ -73,6 +74,42 @@ def test_block_through_launcher(backend, dev, tmp_path):
     assert (folder / "lwp.json").exists() and (folder / "perf.txt").exists() and (folder / "block.plan.txt").exists()
     back = backend.read_output_tensor(folder / "_mlir_ciface_block_o0.raw")
     assert torch.equal(back, outs[0])
+    # LWP: region 0 is the whole run, regions 1..n the planned ops, each
+    # closed once, nested in region 0, with non-negative GPU time
+    lwp = json.loads((folder / "lwp.json").read_text())
+    summary = fold_lwp(lwp["entries"])
+    n_ops = len(summary) - 1
+    assert n_ops >= len(pats) and set(summary) == set(range(n_ops + 1))
+    assert all(cnt == 1 for _, cnt, _ in summary.values())
+    assert all(summary[i][2] == 0 for i in range(1, n_ops + 1)) and summary[0][2] is None
+    assert all(tot >= 0 for tot, _, _ in summary.values())
+    assert sum(summary[i][0] for i in range(1, n_ops + 1)) <= summary[0][0]
+    assert lwp["cyc_hz"] > 0
+    # the run takes between 1 us and 1 s of GPU time
+    assert 1e-6 <= summary[0][0] / lwp["cyc_hz"] <= 1.0
+    dump = (folder / "lwp_infodump.txt").read_text().strip().split("\n")
+    ids = sorted(int(re.search(r"corresponds to ID (\d+)", line).group(1)) for line in dump)
+    assert ids == list(range(n_ops + 1))
+
+
+def test_tile_sizes_apply_to_their_run_only(backend, pkg, dev, tmp_path):
+    """tileSizes forces the GEMM tile of the runs of that plan and nothing
+    else: no environment variable, no thread override left behind."""
+    import os
+
+    a, b = uniform((256, 512), 20), uniform((512, 384), 21)
+    path = str(tmp_path / "mm.pt2")
+    model = MatMul()
+    backend.write_program_to_file(backend.export_program(model, [a, b]), path)
+    launcher = backend.TorchMLIRHexagonLauncher()
+    opts = backend.HexagonOptions(tileSizes="64,64").__dict__
+    out = launcher.run_torch_mlir(path, [a, b], "mm", str(tmp_path), options=opts)
+    assert launcher.last_plan.gemm_tile is not None
+    assert "HXMI_GEMM_TILE" not in os.environ
+    assert pkg.set_tuning("gemm_tile", None) is None  # no override left on this thread
+    plain = backend.TorchMLIRHexagonLauncher().run_torch_mlir(path, [a, b], "mm2", str(tmp_path))
+    assert ref.max_rel_err(np32(out[0]), ref.matmul(a.numpy(), b.numpy())) <= TOL
+    assert ref.max_rel_err(np32(plain[0]), ref.matmul(a.numpy(), b.numpy())) <= TOL
 
 
 def test_fusion_off_gives_same_numbers(backend, dev, tmp_path):
