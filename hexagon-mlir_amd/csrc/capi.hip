@@ -4,10 +4,40 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/hxmi.h"
 #include "hxmi_internal.h"
 
+// Split-K scratch of hxmi_gemm_f16_noalloc: one array per GPU, in the code
+// object's zero-filled data, so its arrival counters start at zero and every
+// call leaves them zero.  In host code `scratch` names a host-side stand-in,
+// not the device array: kernels get the address from hipGetSymbolAddress.
+static __device__ __align__(256) char scratch[HXMI_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+std::once_flag g_scratch_once[kMaxDevices];
+
+// Device address of the current device's scratch array, looked up once per
+// device (with that device current).
+hipError_t scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess) return g_scratch_err[dev];
+  *out = g_scratch_ptr[dev];
+  return *out ? hipSuccess : hipErrorInvalidSymbol;
+}
 
 thread_local char g_err[512] = "";
 
@@ -39,7 +69,7 @@ int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bi
                 int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB, int64_t sC,
                 int b_is_nt, int epilogue, float alpha, int out_f32, void* ws, int64_t ws_bytes, void* stream,
                 const char* name, int rms = 0, float rms_eps = 0.f, float* rs_out = nullptr,
-                const float* rs_in = nullptr) {
+                const float* rs_in = nullptr, bool noalloc = false) {
   REQUIRE(batch >= 0 && M >= 0 && N >= 0 && K >= 0, "%s: negative size (batch=%lld M=%lld N=%lld K=%lld)", name,
           (long long)batch, (long long)M, (long long)N, (long long)K);
   REQUIRE(b_is_nt == 0 || b_is_nt == 1, "%s: b_is_nt must be 0 or 1", name);
@@ -82,6 +112,21 @@ int gemm_common(int dtype, const void* A, const void* B, void* C, const void* bi
   p.rms_eps = rms_eps;
   p.rs_out = rs_out;
   p.rs_in = rs_in;
+  if (noalloc) {
+    // the split-K partials go to this device's scratch array
+    const int64_t need = hxmi::gemm_workspace_bytes(p);
+    REQUIRE(need <= (int64_t)HXMI_NOALLOC_SCRATCH_BYTES,
+            "%s: this shape's split-K partials need %lld bytes, more than the %lld-byte device scratch (call "
+            "hxmi_gemm_f16 with a workspace instead)",
+            name, (long long)need, (long long)HXMI_NOALLOC_SCRATCH_BYTES);
+    if (need > 0) {
+      void* s = nullptr;
+      const hipError_t e = scratch_ptr(&s);
+      if (e != hipSuccess) return from_hip(e, name);
+      p.ws = s;
+      p.ws_bytes = HXMI_NOALLOC_SCRATCH_BYTES;
+    }
+  }
   return from_hip(hxmi::launch_gemm(p, (hipStream_t)stream), name);
 }
 
@@ -137,6 +182,13 @@ int hxmi_gemm_bf16(const void* A, const void* B, void* C, const void* bias, int6
                    int64_t workspace_bytes, void* stream) {
   return gemm_common(hxmi::DT_BF16, A, B, C, bias, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, b_is_nt, epilogue, alpha, 0,
                      workspace, workspace_bytes, stream, "hxmi_gemm_bf16");
+}
+
+int hxmi_gemm_f16_noalloc(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                          int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha,
+                          void* stream) {
+  return gemm_common(hxmi::DT_F16, A, B, C, bias, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, b_is_nt, epilogue, alpha, 0,
+                     nullptr, 0, stream, "hxmi_gemm_f16_noalloc", 0, 0.f, nullptr, nullptr, true);
 }
 
 int64_t hxmi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_is_nt, int epilogue) {

@@ -38,6 +38,7 @@ SIGNATURES = {
     "hxmi_gemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P], _I),
     "hxmi_gemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P, _I64, _P], _I),
     "hxmi_gemm_workspace_bytes": ([_I64, _I64, _I64, _I, _I], _I64),
+    "hxmi_gemm_f16_noalloc": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_bgemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_bgemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),

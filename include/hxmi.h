@@ -114,6 +114,30 @@ int hxmi_gemm_bf16(const void* A, const void* B, void* C, const void* bias, int6
  * (0: it never splits K).  Depends on shapes and epilogue only. */
 int64_t hxmi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int b_is_nt, int epilogue);
 
+/* Bytes of the per-GPU device scratch array hxmi_gemm_f16_noalloc uses. */
+#define HXMI_NOALLOC_SCRATCH_BYTES 33554432
+
+/*
+ * hxmi_gemm_f16 without a workspace argument and without any allocation:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, results and epilogues as hxmi_gemm_f16; where that call would
+ * split K, the fp32 partial tiles go to a library-owned array of
+ * HXMI_NOALLOC_SCRATCH_BYTES in each GPU's memory (held until the process
+ * ends) instead of a caller workspace.  A shape whose partials need more is
+ * rejected with HXMI_ERR_INVALID_ARGUMENT before anything is launched.  The
+ * array's arrival counters start zero and every call leaves them zero.  All
+ * calls on one GPU share its array: two calls whose executions overlap on
+ * one GPU (different streams, or concurrent graph replays) race and give
+ * wrong results; calls ordered on one stream are safe.  `stream` must
+ * belong to the current device.
+ * No counterpart in the reference (its kernels allocate VTCM from a runtime
+ * pool, VTCMPool.cpp:62-106); it exists for the callers named above.
+ */
+int hxmi_gemm_f16_noalloc(const void* A, const void* B, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                          int64_t lda, int64_t ldb, int64_t ldc, int b_is_nt, int epilogue, float alpha,
+                          void* stream);
+
 /*
  * Strided batched GEMM: for b in [0,batch): C + b*strideC = epilogue(alpha *
  * (A + b*strideA) . op(B + b*strideB)).  Strides in elements.

@@ -182,3 +182,15 @@ def test_plan_tile_applies_to_its_own_runs_only(pkg):
     Plan(module=Probe())(1)
     assert seen == [6, None]
     assert pkg.set_tuning("gemm_tile", None) is None
+
+
+def test_noalloc_gemm_rejects_partials_beyond_its_scratch(pkg):
+    """A forced 4-way K split of 1216 x 2560 x 8192 needs ~50 MB of partials,
+    more than the 32 MiB scratch: rejected before any launch."""
+    lib = pkg.load_library()
+    fake = 1 << 12  # aligned, never dereferenced: the call fails its size check first
+    with pkg.tuning(splitk=4):
+        rc = lib.hxmi_gemm_f16_noalloc(fake, fake, fake, None, 1216, 2560, 8192, 8192, 8192, 2560, 1, 0, 1.0, None)
+        msg = lib.hxmi_last_error()  # (the next successful call clears it)
+    assert rc == 1
+    assert b"device scratch" in msg
