@@ -24,7 +24,8 @@ in the plan):
                  packed gate/up weight with the SiLU-mul epilogue
   linear_gelu    gelu(linear(x, W, b), approximate="tanh") -> GEMM + epilogue
   attention      matmul(softmax(matmul(q, k^T) * s), v) and
-                 scaled_dot_product_attention (no mask / dropout / causal)
+                 scaled_dot_product_attention (additive or boolean mask,
+                 is_causal, grouped K/V heads; no dropout)
   linear, matmul, bmm, mm, addmm, softmax(-1) -> GEMM / row kernels
 """
 from __future__ import annotations
@@ -115,8 +116,8 @@ def hx_softmax(x):
     return _pkg().softmax(x.contiguous())
 
 
-def hx_attention(q, k, v, scale):
-    return _pkg().attention(q.contiguous(), k.contiguous(), v.contiguous(), scale)
+def hx_attention(q, k, v, scale, mask=None, causal=0):
+    return _pkg().attention(q.contiguous(), k.contiguous(), v.contiguous(), scale, mask=mask, causal=causal)
 
 
 # ---- planning -------------------------------------------------------------------------
@@ -354,14 +355,23 @@ class _Planner:
         for n in list(self.g.nodes):
             if not (_is(n, aten.scaled_dot_product_attention.default) and _is_half(n)):
                 continue
-            if len(n.args) > 3 and n.args[3] is not None or n.kwargs.get("attn_mask") is not None:
+            arg = lambda i, name, dflt: n.kwargs.get(name, n.args[i] if len(n.args) > i else dflt)  # noqa: E731
+            mask, causal = arg(3, "attn_mask", None), bool(arg(5, "is_causal", False))
+            if arg(4, "dropout_p", 0.0):
                 continue
-            if n.kwargs.get("dropout_p", n.args[4] if len(n.args) > 4 else 0.0) or \
-                    n.kwargs.get("is_causal", n.args[5] if len(n.args) > 5 else False):
+            q, k, v = (_val(x) for x in n.args[:3])
+            scale = arg(6, "scale", None) or 1.0 / math.sqrt(q.shape[-1])
+            gqa = k.shape[-3] != q.shape[-3]
+            # masked, causal and grouped-query SDPA need the fused kernel's shapes; the rest stays on torch
+            if (mask is not None or causal or gqa) and not (q.shape[-1] in (64, 128) and v.shape[-1] == q.shape[-1]
+                                                            and scale > 0):
                 continue
-            q = n.args[0]
-            scale = n.kwargs.get("scale") or 1.0 / math.sqrt(_val(q).shape[-1])
-            self.replace(n, hx_attention, (n.args[0], n.args[1], n.args[2], float(scale)), "attention")
+            if gqa and not arg(7, "enable_gqa", False):
+                continue
+            if mask is not None and _val(mask).dtype not in (torch.bool, torch.float16):
+                continue
+            self.replace(n, hx_attention, (n.args[0], n.args[1], n.args[2], float(scale), mask, int(causal)),
+                         "attention")
 
     def single_ops(self):
         for n in list(self.g.nodes):

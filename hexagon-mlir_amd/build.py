@@ -33,6 +33,13 @@ HIPFLAGS = [
 ]
 
 
+# Per-source extra flags.  attention.hip rescales its MFMA accumulators with
+# vector ALU ops between MFMAs; with accumulators in AGPRs (the compiler's
+# default) every key block copies them to VGPRs and back, so that file asks
+# for the VGPR form of the MFMA operands.
+EXTRA = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -42,7 +49,7 @@ def hipcc() -> str:
 
 def _compile(src: pathlib.Path) -> pathlib.Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPFLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")

@@ -339,26 +339,41 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
                     "hxmi_softmax_bf16");
 }
 
-int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q, int64_t s_kv,
-                       int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t stride_q,
-                       int64_t stride_k, int64_t stride_v, int64_t stride_o, float scale, void* stream) {
-  const char* name = "hxmi_attention_f16";
+namespace {
+int attention_common(const char* name, const void* q, const void* k, const void* v, void* o, int64_t bh,
+                     int64_t s_q, int64_t s_kv, int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                     int64_t stride_q, int64_t stride_k, int64_t stride_v, int64_t stride_o, int64_t kv_group,
+                     const void* mask, int64_t ldm, int64_t stride_m, int64_t mask_group, int causal, float scale,
+                     void* stream) {
   REQUIRE(bh >= 0 && s_q >= 0 && s_kv >= 0 && d >= 0, "%s: negative size", name);
   if (bh == 0 || s_q == 0) return ok();
   REQUIRE(s_kv > 0, "%s: softmax over zero keys", name);
   REQUIRE(d == 64 || d == 128, "%s: head dim %lld unsupported (64 or 128)", name, (long long)d);
   REQUIRE(q && k && v && o, "%s: null pointer", name);
+  REQUIRE(scale > 0.f && scale < INFINITY, "%s: scale must be positive and finite", name);
+  REQUIRE(kv_group >= 1 && bh % kv_group == 0, "%s: kv_group %lld must divide bh %lld", name, (long long)kv_group,
+          (long long)bh);
+  REQUIRE(causal >= 0 && causal <= 2, "%s: causal %d (0 none, 1 top-left, 2 bottom-right)", name, causal);
   REQUIRE(ldq >= d && ldk >= d && ldv >= d && ldo >= d, "%s: leading dimension smaller than head dim", name);
   REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 && stride_q % 8 == 0 && stride_k % 8 == 0 &&
               stride_v % 8 == 0 && stride_o % 4 == 0,
           "%s: strides must keep 16-byte aligned rows", name);
   REQUIRE(al(q, 16) && al(k, 16) && al(v, 16) && al(o, 8), "%s: q, k, v need 16-byte, o 8-byte alignment", name);
   REQUIRE(s_q < (1ll << 30) && s_kv < (1ll << 30), "%s: sequence too long", name);
+  REQUIRE(((s_kv - 1) * ldk + d) * 2 <= (1ll << 31) && ((s_kv - 1) * ldv + d) * 2 <= (1ll << 31),
+          "%s: one K or V slice must span at most 2 GiB", name);
+  if (mask) {
+    REQUIRE(ldm >= s_kv && stride_m >= 0, "%s: mask row stride %lld below s_kv", name, (long long)ldm);
+    REQUIRE(mask_group >= 1 && bh % mask_group == 0, "%s: mask_group %lld must divide bh", name,
+            (long long)mask_group);
+    REQUIRE(al(mask, 2), "%s: mask needs 2-byte alignment", name);
+  }
   hxmi::AttnProblem p{};
   p.q = q;
   p.k = k;
   p.v = v;
   p.o = o;
+  p.mask = mask;
   p.bh = bh;
   p.s = s_q;
   p.skv = s_kv;
@@ -367,12 +382,35 @@ int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int
   p.ldk = ldk;
   p.ldv = ldv;
   p.ldo = ldo;
+  p.ldm = ldm;
   p.sq = stride_q;
   p.sk = stride_k;
   p.sv = stride_v;
   p.so = stride_o;
+  p.sm = stride_m;
+  p.kv_group = kv_group;
+  p.mask_group = mask ? mask_group : 1;
+  p.causal = causal;
   p.scale = scale;
   return from_hip(hxmi::launch_attention(p, (hipStream_t)stream), name);
+}
+}  // namespace
+
+int hxmi_attention_ex_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q,
+                          int64_t s_kv, int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                          int64_t stride_q, int64_t stride_k, int64_t stride_v, int64_t stride_o, int64_t kv_group,
+                          const void* mask, int64_t ldm, int64_t stride_m, int64_t mask_group, int causal,
+                          float scale, void* stream) {
+  return attention_common("hxmi_attention_ex_f16", q, k, v, o, bh, s_q, s_kv, d, ldq, ldk, ldv, ldo, stride_q,
+                          stride_k, stride_v, stride_o, kv_group, mask, ldm, stride_m, mask_group, causal, scale,
+                          stream);
+}
+
+int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q, int64_t s_kv,
+                       int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t stride_q,
+                       int64_t stride_k, int64_t stride_v, int64_t stride_o, float scale, void* stream) {
+  return attention_common("hxmi_attention_f16", q, k, v, o, bh, s_q, s_kv, d, ldq, ldk, ldv, ldo, stride_q, stride_k,
+                          stride_v, stride_o, 1, nullptr, 0, 0, 1, 0, scale, stream);
 }
 
 int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N, int64_t K,

@@ -41,6 +41,7 @@ enum Knob {
   KNOB_GEMV_KG,        // workgroups splitting K per GEMV row group
   KNOB_GEMV_UNR,       // K-steps in flight per GEMV wave
   KNOB_GEMV_PAIR_WG,   // workgroup cap of the whole-line GEMV
+  KNOB_ATTN_CFG,       // fused attention: 10 * query waves + key-split waves per workgroup
   KNOB_COUNT
 };
 enum GemvPath { GEMV_PATH_MFMA = 0, GEMV_PATH_VALU = 1, GEMV_PATH_PAIR = 2, GEMV_PATH_PAIR_KS = 3 };
@@ -155,12 +156,16 @@ hipError_t launch_softmax(const RowProblem& p, hipStream_t stream);
 
 struct AttnProblem {
   const void* q;  // [B*H, S, D]
-  const void* k;  // [B*H, SKV, D]
+  const void* k;  // [B*H / kv_group, SKV, D]
   const void* v;
   void* o;
+  const void* mask;  // fp16 additive [B*H / mask_group, S, SKV] or null
   int64_t bh, s, skv, d;
-  int64_t sq, sk, sv, so;  // per-(b,h) strides, elements
-  int64_t ldq, ldk, ldv, ldo;
+  int64_t sq, sk, sv, so, sm;  // per-slice strides, elements
+  int64_t ldq, ldk, ldv, ldo, ldm;
+  int64_t kv_group;    // query heads per key/value head
+  int64_t mask_group;  // (batch, head) slices sharing one mask slice
+  int causal;          // 0 none, 1 key <= query, 2 key <= query + skv - s
   float scale;
 };
 

@@ -22,13 +22,14 @@ constexpr KnobInfo kKnobs[KNOB_COUNT] = {
     {"gemm_tile", "HXMI_GEMM_TILE"}, {"group_m", "HXMI_GROUP_M"},     {"splitk", "HXMI_SPLITK"},
     {"w8_tile", "HXMI_W8_TILE"},     {"gemv_path", "HXMI_GEMV_PATH"}, {"gemv_tpb", "HXMI_GEMV_TPB"},
     {"gemv_ks", "HXMI_GEMV_KS"},     {"gemv_kg", "HXMI_GEMV_KG"},     {"gemv_unr", "HXMI_GEMV_UNR"},
-    {"gemv_pair_wg", "HXMI_GEMV_PAIR_WG"},
+    {"gemv_pair_wg", "HXMI_GEMV_PAIR_WG"}, {"attn_cfg", "HXMI_ATTN_CFG"},
 };
 
 int64_t g_env[KNOB_COUNT];
-thread_local int64_t t_over[KNOB_COUNT] = {KNOB_UNSET, KNOB_UNSET, KNOB_UNSET, KNOB_UNSET, KNOB_UNSET,
-                                           KNOB_UNSET, KNOB_UNSET, KNOB_UNSET, KNOB_UNSET, KNOB_UNSET};
-static_assert(KNOB_COUNT == 10, "t_over initialiser");
+thread_local int64_t t_over[KNOB_COUNT] = {KNOB_UNSET, KNOB_UNSET, KNOB_UNSET, KNOB_UNSET,
+                                           KNOB_UNSET, KNOB_UNSET, KNOB_UNSET, KNOB_UNSET,
+                                           KNOB_UNSET, KNOB_UNSET, KNOB_UNSET};
+static_assert(KNOB_COUNT == 11, "t_over initialiser");
 
 // HXMI_GEMV_PATH names a kernel by its first letter: valu, pair, k-split
 // pair; anything else is the 16-row MFMA kernel

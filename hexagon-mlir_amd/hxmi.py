@@ -50,6 +50,7 @@ SIGNATURES = {
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
+    "hxmi_attention_ex_f16": ([_P, _P, _P, _P] + [_I64] * 13 + [_P, _I64, _I64, _I64, _I, _F, _P], _I),
     "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_quantize_int8_rows_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
@@ -469,21 +470,56 @@ def softmax(x: torch.Tensor, scale: float = 1.0, out: Optional[torch.Tensor] = N
     return out2.reshape(*lead, cols)
 
 
+def _mask_slices(mask: torch.Tensor, lead: tuple, S: int, Skv: int) -> tuple[torch.Tensor, int, int, int]:
+    """An additive fp16 mask broadcast over the leading dims as (tensor, ldm,
+    slice stride, slices per mask slice).  A boolean mask keeps the True
+    entries (0) and removes the others (-inf), as torch's SDPA reads it."""
+    if mask.dtype == torch.bool:
+        mask = torch.zeros(mask.shape, dtype=torch.float16, device=mask.device).masked_fill_(~mask, float("-inf"))
+    elif mask.dtype != torch.float16:
+        mask = mask.to(torch.float16)
+    try:
+        m = mask.expand(*lead, S, Skv)
+    except RuntimeError:
+        raise HxmiError(f"mask of shape {tuple(mask.shape)} does not broadcast to {(*lead, S, Skv)}") from None
+    if m.stride(-1) != 1 or m.data_ptr() % 2:
+        m = m.contiguous()
+    st = m.stride()[:-2]
+    if all(x == 0 for x in st):
+        return m, m.stride(-2), 0, 1
+    if len(lead) >= 2 and st[-1] == 0 and all(st[i] == st[i + 1] * lead[i + 1] for i in range(len(lead) - 2)):
+        return m, m.stride(-2), st[-2], lead[-1]  # [..., B, 1, S, Skv]: one slice per row of heads
+    if all(st[i] == st[i + 1] * lead[i + 1] for i in range(len(lead) - 1)):
+        return m, m.stride(-2), st[-1], 1
+    m = m.contiguous()
+    return m, Skv, S * Skv, 1
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
-              out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """SDPA as the reference lowers it (LowerTmTensor.cpp:91-250): softmax(scale * Q.K^T) . V over
-    q [..., S, D], k and v [..., S_kv, D].  fp16 with D in {64, 128} runs the fused kernel
-    (hxmi_attention_f16); other cases run the same three steps as bmm(Q, K^T) -> softmax -> bmm(P, V)."""
+              out: Optional[torch.Tensor] = None, *, mask: Optional[torch.Tensor] = None,
+              causal: int = 0) -> torch.Tensor:
+    """SDPA as the reference lowers it (LowerTmTensor.cpp:91-250): softmax(scale * Q.K^T + mask) . V over
+    q [..., S, D], k and v [..., S_kv, D].  K/V may have fewer slices than q in their last leading dim
+    (grouped-query attention: that many q heads per kv head).  mask: additive (or boolean keep) mask
+    broadcastable to [..., S, S_kv]; causal: 1 masks keys after the query (torch's is_causal), 2 after
+    query + S_kv - S.  fp16 with D in {64, 128} and scale > 0 runs the fused kernel (hxmi_attention_ex_f16);
+    other unmasked cases run the reference's three steps as bmm(Q, K^T) -> softmax -> bmm(P, V)."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    lead = q.shape[:-2]
     S, D = q.shape[-2:]
-    if k.shape[-1] != D or k.shape[:-2] != lead or v.shape[:-2] != lead or v.shape[-2] != k.shape[-2]:
+    Skv = k.shape[-2]
+    lead = tuple(q.shape[:-2])
+    if q.dim() < 3 or k.dim() != q.dim() or v.dim() != q.dim() or k.shape[-1] != D or v.shape[-2] != Skv \
+            or k.shape[:-3] != q.shape[:-3] or v.shape[:-2] != k.shape[:-2] or q.shape[-3] % max(k.shape[-3], 1):
         raise HxmiError(f"attention shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    group = q.shape[-3] // k.shape[-3] if k.shape[-3] else 1
+    if causal not in (0, 1, 2, False, True):
+        raise HxmiError(f"causal must be 0, 1 or 2, got {causal}")
     q3 = q.reshape(-1, S, D)
-    k3 = k.reshape(-1, k.shape[-2], D)
-    v3 = v.reshape(-1, v.shape[-2], v.shape[-1])
-    if q.dtype == torch.float16 and D in (64, 128) and v.shape[-1] == D and k.dtype == v.dtype == q.dtype:
+    k3 = k.reshape(-1, Skv, D)
+    v3 = v.reshape(-1, Skv, v.shape[-1])
+    if q.dtype == torch.float16 and D in (64, 128) and v.shape[-1] == D and k.dtype == v.dtype == q.dtype \
+            and scale > 0:
         _require_gpu(q3, k3, v3)
         q3, k3, v3 = (t if t.stride(-1) == 1 and t.stride(1) % 8 == 0 and t.stride(0) % 8 == 0
                       and t.data_ptr() % 16 == 0 else t.contiguous() for t in (q3, k3, v3))
@@ -501,10 +537,18 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional
         ldk, bk = _batched(k3, "k")
         ldv, bv = _batched(v3, "v")
         ldo, bo = _batched(o, "out")
-        _check(load_library().hxmi_attention_f16(q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), o.data_ptr(),
-                                                 q3.shape[0], S, k3.shape[1], D, ldq, ldk, ldv, ldo, bq, bk, bv,
-                                                 bo, float(scale), _stream(q)))
+        mp, ldm, sm, mg = 0, 0, 0, 1
+        if mask is not None:
+            _require_gpu(mask)
+            m, ldm, sm, mg = _mask_slices(mask, lead, S, Skv)
+            mp = m.data_ptr()
+        _check(load_library().hxmi_attention_ex_f16(q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), o.data_ptr(),
+                                                    q3.shape[0], S, Skv, D, ldq, ldk, ldv, ldo, bq, bk, bv, bo,
+                                                    group, mp, ldm, sm, mg, int(causal), float(scale), _stream(q)))
         return out if out is not None else o.reshape(*lead, S, D)
+    if mask is not None or causal or group != 1:
+        raise HxmiError("masked, causal and grouped-query attention run on the fused kernel only "
+                        "(fp16, head dim 64 or 128, scale > 0)")
     s = bgemm(q3, k3, b_layout="nt", alpha=scale)
     p = softmax(s)
     if out is not None:

@@ -264,7 +264,8 @@ int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, in
  * Fused attention, fp16: for each of bh (batch x head) slices,
  *   O[i] = softmax(scale * Q[i] . K^T) . V  over s_kv keys,
  * Q/O [s_q, d], K/V [s_kv, d] row-major (leading dims ld*, slice strides
- * stride_*, elements), d = 64 or 128, fp32 softmax and accumulation, no mask.
+ * stride_*, elements), d = 64 or 128, scale > 0, fp32 softmax and accumulation,
+ * no mask.
  * Replaces: tm_tensor.attention as LowerTmTensor.cpp:52-250 lowers it
  * (batch_matmul(Q, K^T) -> scale -> softmax -> batch_matmul(P, V), semantics
  * of qcom_hexagon_backend/test/Conversion/TmTensorToLinalg/SDPA.mlir:18-59)
@@ -274,6 +275,34 @@ int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, in
 int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q, int64_t s_kv,
                        int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t stride_q,
                        int64_t stride_k, int64_t stride_v, int64_t stride_o, float scale, void* stream);
+
+/*
+ * Fused attention with the reference's mask operand, fp16:
+ *   O[i] = softmax(scale * Q[i] . K[i / kv_group]^T + M[i / mask_group]) . V[i / kv_group]
+ * with, when causal != 0, every key j of query r with j > r (causal = 1, the
+ * top-left rule of torch's is_causal) or j > r + s_kv - s_q (causal = 2,
+ * bottom-right) masked to -inf.
+ *  - mask: fp16 additive [s_q, s_kv] per slice (row stride ldm >= s_kv, slice
+ *    stride stride_m, 0 broadcasts one slice to all), or NULL for none; -inf
+ *    entries remove a key.  mask_group consecutive (batch, head) slices share
+ *    one mask slice (e.g. the heads of one batch row for a [B, 1, S, S_kv]
+ *    mask).
+ *  - kv_group consecutive query slices share one K/V slice (grouped-query
+ *    attention: q heads per kv head; 1 = one K/V slice per query slice);
+ *    stride_k / stride_v step between K/V slices.
+ *  - scale > 0.  A query whose every key is masked yields NaN (0/0), as the
+ *    reference's decomposition does.
+ * Other arguments as hxmi_attention_f16, which equals kv_group = 1, no mask,
+ * causal = 0.
+ * Replaces: tm_tensor.attention with its mask operand
+ * (LowerTmTensor.cpp:81-88 reads it, :158-163 adds it to the scaled Q.K^T
+ * before the softmax).
+ */
+int hxmi_attention_ex_f16(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t s_q,
+                          int64_t s_kv, int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                          int64_t stride_q, int64_t stride_k, int64_t stride_v, int64_t stride_o, int64_t kv_group,
+                          const void* mask, int64_t ldm, int64_t stride_m, int64_t mask_group, int causal,
+                          float scale, void* stream);
 
 /*
  * Region profiling hook: enqueues on `stream` a one-wave marker that, when it

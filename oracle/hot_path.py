@@ -30,7 +30,11 @@ Parity status per function (how each is pinned, see tests/test_oracle.py):
                               scale against a brute-force search over every
                               fp16 value, sign symmetry and power-of-two
                               equivariance
-  sdpa                        composition of the above vs torch SDPA math
+  sdpa                        torch F.scaled_dot_product_attention (fp32 CPU)
+                              with and without an additive / boolean mask,
+                              is_causal, enable_gqa and torch's lower-right
+                              causal bias; one-hot and fully-masked closed
+                              forms; mask shift invariance
   vtcm_tile_sizes             the reference's lit expectation
                               (vtcm_tiling_static.mlir:80-88) and the
                               footprint rule it encodes
@@ -174,16 +178,35 @@ def softmax(x, scale: float = 1.0) -> np.ndarray:
     return e / np.sum(e, axis=-1, keepdims=True)
 
 
-def sdpa(q, k, v, scale=None) -> np.ndarray:
+def sdpa(q, k, v, scale=None, mask=None, causal: int = 0, kv_group: int = 1) -> np.ndarray:
     """Attention as lib/Transforms/LowerTmTensor.cpp:91-250 lowers
-    tm_tensor.attention: bmm(Q, K^T) * scale -> softmax -> bmm(P, V)
+    tm_tensor.attention: bmm(Q, K^T) * scale (:130-145) + mask (:158-163) ->
+    softmax (max, exp(x - max), sum, div: :165-229) -> bmm(P, V)
     (scale 1/sqrt(d), qcom_hexagon_backend/test/Conversion/TmTensorToLinalg/
-    SDPA.mlir:18-31)."""
+    SDPA.mlir:18-31).  q [..., S, D], k and v [..., S_kv, D]; mask is added
+    to the scaled scores (broadcast over the leading dims); causal = 1 masks
+    key j of query i when j > i (torch's is_causal), causal = 2 when
+    j > i + S_kv - S; kv_group consecutive query slices of the leading
+    dims' last axis share one K/V slice.  A row whose every entry is -inf
+    comes out NaN, as exp(x - max) over it does in the decomposition."""
+    q32, k32, v32 = _f32(q), _f32(k), _f32(v)
     if scale is None:
-        scale = 1.0 / math.sqrt(np.asarray(q).shape[-1])
-    s = bmm(q, k, "nt")
-    p = softmax(s, scale)
-    return np.matmul(p, _f32(v))
+        scale = 1.0 / math.sqrt(q32.shape[-1])
+    if kv_group > 1:
+        k32 = np.repeat(k32, kv_group, axis=-3)
+        v32 = np.repeat(v32, kv_group, axis=-3)
+    z = bmm(q32, k32, "nt") * F32(scale)
+    if mask is not None:
+        z = z + _f32(mask)
+    if causal:
+        sq, skv = z.shape[-2:]
+        off = 0 if causal == 1 else skv - sq
+        z = np.where(np.arange(skv)[None, :] > np.arange(sq)[:, None] + off, F32(-np.inf), z)
+    with np.errstate(invalid="ignore"):
+        z = z - np.max(z, axis=-1, keepdims=True)
+        e = np.exp(z)
+        p = e / np.sum(e, axis=-1, keepdims=True)
+    return np.matmul(p, v32)
 
 
 # ---- weight-only int8 ----------------------------------------------------------------

@@ -166,8 +166,13 @@ class OraclePkg(types.SimpleNamespace):
         return torch.from_numpy(y).half().reshape(*lead, y.shape[-1])
 
     @staticmethod
-    def attention(q, k, v, scale):
-        return torch.from_numpy(ref.sdpa(q.numpy(), k.numpy(), v.numpy(), scale)).half()
+    def attention(q, k, v, scale, mask=None, causal=0):
+        if mask is not None and mask.dtype == torch.bool:
+            mask = torch.where(mask, 0.0, float("-inf"))
+        m = None if mask is None else mask.float().numpy()
+        out = ref.sdpa(q.numpy(), k.numpy(), v.numpy(), scale, mask=m, causal=causal,
+                       kv_group=q.shape[-3] // k.shape[-3])
+        return torch.from_numpy(out).half()
 
     @staticmethod
     def pack_gate_up(wg, wu):
@@ -229,6 +234,36 @@ def test_planner_matches_hot_path_patterns(backend, oracle_kernels):
     left = " ".join(plan.torch_ops)
     for op in ("linear", "matmul", "softmax", "rsqrt", "silu", "gelu", "rms_norm", "scaled_dot"):
         assert op not in left, left
+
+
+class MaskedAttn(nn.Module):
+    """Decoder-style attention calls: a padding mask, a causal one over
+    grouped K/V heads, and one the fused kernel cannot take (head dim 8)."""
+
+    def forward(self, q, k, v, kg, vg, m, q8, k8, v8, m8):
+        a = F.scaled_dot_product_attention(q, k, v, attn_mask=m)
+        b = F.scaled_dot_product_attention(q, kg, vg, is_causal=True, enable_gqa=True)
+        c = F.scaled_dot_product_attention(q8, k8, v8, attn_mask=m8)
+        return a, b, c
+
+
+def test_planner_routes_masked_causal_gqa_attention(backend, oracle_kernels):
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, 4, 16, 64, generator=g).half() for _ in range(3))
+    kg, vg = (torch.randn(1, 2, 16, 64, generator=g).half() for _ in range(2))
+    m = torch.zeros(1, 1, 16, 16).half()
+    m[..., 12:] = float("-inf")
+    q8, k8, v8 = (torch.randn(1, 2, 16, 8, generator=g).half() for _ in range(3))
+    m8 = torch.zeros(16, 16).half()
+    args = [q, k, v, kg, vg, m, q8, k8, v8, m8]
+    ep = backend.export_program(MaskedAttn(), args)
+    plan = backend.plan_program(ep, torch.device("cpu"), fusion=True)
+    assert sorted(p for p, _ in plan.kernels) == ["attention", "attention"]
+    assert sum("scaled_dot" in t for t in plan.torch_ops) == 1  # head dim 8 with a mask stays on torch
+    a, b, _ = plan(*args)
+    ex = lambda x: x.float().numpy()  # noqa: E731
+    assert ref.max_err_vs_scale(ex(a), ref.sdpa(ex(q), ex(k), ex(v), mask=ex(m))) < 1e-2
+    assert ref.max_err_vs_scale(ex(b), ref.sdpa(ex(q), ex(kg), ex(vg), causal=1, kv_group=2)) < 1e-2
 
 
 def test_planner_without_fusion_keeps_elementwise_ops(backend, oracle_kernels):

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import TOL, np32, uniform
+from gpu_util import TOL, normal, np32, uniform
 from oracle import hot_path as ref
 
 pytestmark = pytest.mark.gpu
@@ -109,3 +109,141 @@ def test_attention_rejects_bad_head_dim_through_abi(pkg, dev):
     rc = lib.hxmi_attention_f16(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 4, 4, 96, 96, 96, 96, 96,
                                 0, 0, 0, 0, 1.0, None)
     assert rc == 1 and b"head dim" in lib.hxmi_last_error()
+
+
+# ---- mask operand, causal rules, grouped K/V heads ---------------------------------------------------
+
+CFGS_64 = [41, 22, 14, 21, 12, 42, 24]  # query waves * 10 + key-split waves
+CFGS_128 = [41, 22, 14, 21, 12]
+
+
+def _check_nan(out, exp):
+    """As _check, where rows whose every key is masked must be NaN in both."""
+    o = np32(out)
+    nan_e = np.isnan(exp).all(-1)
+    assert np.array_equal(np.isnan(o).all(-1), nan_e) and not np.isnan(o[~nan_e]).any()
+    o, exp = o[~nan_e], exp[~nan_e]
+    assert ref.max_err_vs_scale(o, exp) <= TOL
+    assert np.sqrt(np.mean((o - exp) ** 2)) <= 2e-3 * np.sqrt(np.mean(exp**2)) + 1e-6
+
+
+@pytest.mark.parametrize(
+    "b,h,s,skv,d,mshape",
+    [
+        (2, 3, 197, 197, 64, "b1"),  # HF-style [B, 1, S, S_kv] mask shared by the heads
+        (1, 4, 77, 300, 128, "bh"),  # one mask slice per head
+        (2, 2, 100, 256, 64, "ss"),  # one [S, S_kv] mask for every slice (aligned rows: 8-byte loads)
+        (1, 3, 33, 45, 128, "ss"),
+    ],
+)
+def test_attention_additive_mask(pkg, dev, b, h, s, skv, d, mshape):
+    q, k, v = uniform((b, h, s, d), 51), uniform((b, h, skv, d), 52), uniform((b, h, skv, d), 53)
+    shape = {"b1": (b, 1, s, skv), "bh": (b, h, s, skv), "ss": (s, skv)}[mshape]
+    m = normal(shape, 54)
+    drop = torch.rand(shape, generator=torch.Generator().manual_seed(55)) < 0.2
+    m = m.masked_fill(drop, float("-inf"))
+    m[..., 0] = 0.0  # every query keeps key 0
+    scale = d**-0.5
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), scale, mask=m.cuda()).cpu()
+    exp = ref.sdpa(np32(q), np32(k), np32(v), scale, mask=np32(m))
+    _check_nan(out, exp)
+
+
+def test_attention_bool_mask(pkg, dev):
+    b, h, s, d = 2, 2, 130, 64
+    q, k, v = uniform((b, h, s, d), 61), uniform((b, h, s, d), 62), uniform((b, h, s, d), 63)
+    keep = torch.rand((b, 1, s, s), generator=torch.Generator().manual_seed(64)) > 0.5
+    keep[..., 7] = True
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), mask=keep.cuda()).cpu()
+    add = np.where(keep.numpy(), 0.0, -np.inf).astype(np.float32)
+    _check_nan(out, ref.sdpa(np32(q), np32(k), np32(v), d**-0.5, mask=add))
+
+
+@pytest.mark.parametrize(
+    "bh,s,skv,d,causal",
+    [
+        (4, 300, 300, 64, 1),
+        (2, 512, 512, 128, 1),  # TinyLlama-sized causal prefill head pair
+        (3, 100, 300, 128, 2),  # bottom-right: queries are the last 100 positions
+        (2, 300, 100, 64, 2),  # S > S_kv: the first 200 queries see no key (NaN rows)
+        (2, 45, 197, 64, 1),
+    ],
+)
+def test_attention_causal(pkg, dev, bh, s, skv, d, causal):
+    q, k, v = uniform((bh, s, d), 71), uniform((bh, skv, d), 72), uniform((bh, skv, d), 73)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.1, causal=causal).cpu()
+    _check_nan(out, ref.sdpa(np32(q), np32(k), np32(v), 0.1, causal=causal))
+
+
+def test_attention_causal_with_mask_and_gqa(pkg, dev):
+    """TinyLlama's attention shape: 32 query heads over 4 K/V heads, causal, plus a padding mask."""
+    b, hq, hkv, s, d = 1, 32, 4, 256, 64
+    q, k, v = uniform((b, hq, s, d), 81), uniform((b, hkv, s, d), 82), uniform((b, hkv, s, d), 83)
+    m = torch.zeros((b, 1, s, s), dtype=torch.float16)
+    m[..., 200:] = float("-inf")  # padded keys
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), mask=m.cuda(), causal=1).cpu()
+    exp = ref.sdpa(np32(q), np32(k), np32(v), d**-0.5, mask=np32(m), causal=1, kv_group=hq // hkv)
+    _check_nan(out, exp)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 64), (6, 1, 128), (4, 4, 64)])
+def test_attention_gqa(pkg, dev, hq, hkv, d):
+    b, s = 2, 129
+    q, k, v = uniform((b, hq, s, d), 91), uniform((b, hkv, s, d), 92), uniform((b, hkv, s, d), 93)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda()).cpu()
+    _check_nan(out, ref.sdpa(np32(q), np32(k), np32(v), d**-0.5, kv_group=hq // hkv))
+
+
+def test_attention_mask_picks_key_exactly(pkg, dev):
+    """mask[q, t(q)] = +200 makes key t(q) win by far more than fp16 resolves
+    (scores of uniform [-1, 1] inputs stay below 8), so O[q] = V[t(q)] bit for
+    bit: a mask read at a wrong (slice, query, key) shows up.  The mask is
+    [B, 1, S, S_kv], one slice per batch row shared by its heads."""
+    b, h, s, skv, d = 3, 4, 150, 260, 64
+    q, k, v = uniform((b, h, s, d), 101), uniform((b, h, skv, d), 102), uniform((b, h, skv, d), 103)
+    t = torch.randint(0, skv, (b, s), generator=torch.Generator().manual_seed(104))
+    m = torch.zeros((b, 1, s, skv), dtype=torch.float16)
+    m.scatter_(3, t[:, None, :, None], 200.0)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.125, mask=m.cuda()).cpu()
+    want = torch.gather(v, 2, t[:, None, :, None].expand(b, h, s, d))
+    assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("cfg", CFGS_64)
+def test_attention_launch_shapes_d64(pkg, dev, knobs, cfg):
+    """Every workgroup shape (query waves x key-split waves) on the ViT-B/16
+    head shape, unmasked and with a causal padding mask."""
+    knobs(attn_cfg=cfg)
+    bh, s, d = 12, 197, 64
+    q, k, v = uniform((bh, s, d), 111), uniform((bh, s, d), 112), uniform((bh, s, d), 113)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.125).cpu()
+    _check(out, q, k, v, 0.125)
+    m = torch.zeros((s, s), dtype=torch.float16)
+    m[:, 150:] = float("-inf")
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.125, mask=m.cuda(), causal=1).cpu()
+    _check_nan(out, ref.sdpa(np32(q), np32(k), np32(v), 0.125, mask=np32(m), causal=1))
+
+
+@pytest.mark.parametrize("cfg", CFGS_128)
+def test_attention_launch_shapes_d128(pkg, dev, knobs, cfg):
+    knobs(attn_cfg=cfg)
+    bh, s, skv, d = 5, 300, 333, 128
+    q, k, v = uniform((bh, s, d), 121), uniform((bh, skv, d), 122), uniform((bh, skv, d), 123)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.09).cpu()
+    _check(out, q, k, v, 0.09)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.09, causal=2).cpu()
+    _check_nan(out, ref.sdpa(np32(q), np32(k), np32(v), 0.09, causal=2))
+
+
+def test_attention_ex_rejects_bad_arguments(pkg, dev):
+    lib = pkg.hxmi.load_library()
+    x = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
+    args = [x.data_ptr()] * 4 + [2, 4, 4, 64, 64, 64, 64, 64, 256, 256, 256, 256]
+    rc = lib.hxmi_attention_ex_f16(*args, 3, None, 0, 0, 1, 0, 1.0, None)  # kv_group 3 does not divide bh 2
+    assert rc == 1 and b"kv_group" in lib.hxmi_last_error()
+    rc = lib.hxmi_attention_ex_f16(*args, 1, None, 0, 0, 1, 3, 1.0, None)
+    assert rc == 1 and b"causal" in lib.hxmi_last_error()
+    rc = lib.hxmi_attention_ex_f16(*args, 1, None, 0, 0, 1, 0, -1.0, None)
+    assert rc == 1 and b"scale" in lib.hxmi_last_error()
+    rc = lib.hxmi_attention_ex_f16(*args, 1, x.data_ptr(), 2, 0, 1, 0, 1.0, None)  # ldm below s_kv
+    assert rc == 1 and b"mask row stride" in lib.hxmi_last_error()

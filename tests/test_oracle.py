@@ -170,6 +170,58 @@ def test_sdpa_against_torch():
     assert np.allclose(ref.sdpa(q, k, v, 0.125), ref.sdpa(q, k, v, 1 / math.sqrt(64)))
 
 
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x))
+
+
+def test_sdpa_mask_causal_gqa_against_torch():
+    """The mask operand (LowerTmTensor.cpp:158-163), the causal rules and
+    grouped K/V heads against torch's own SDPA on the CPU in fp32."""
+    r = rng(10)
+    b, hq, hkv, s, skv, d = 2, 6, 2, 13, 21, 8
+    q = r.standard_normal((b, hq, s, d)).astype(np.float32)
+    k, v = (r.standard_normal((b, hkv, skv, d)).astype(np.float32) for _ in range(2))
+    m = r.standard_normal((b, 1, s, skv)).astype(np.float32)
+    m[0, 0, 3, 5:9] = -np.inf
+    t = F.scaled_dot_product_attention(_t(q), _t(k), _t(v), attn_mask=_t(m), scale=0.3, enable_gqa=True).numpy()
+    assert np.allclose(ref.sdpa(q, k, v, 0.3, mask=m, kv_group=3), t, atol=1e-5)
+    # boolean mask (True = keep) is the additive mask with 0 / -inf
+    keep = r.random((s, skv)) > 0.3
+    keep[:, 0] = True
+    t = F.scaled_dot_product_attention(_t(q[:, :2]), _t(k), _t(v), attn_mask=_t(keep)).numpy()
+    add = np.where(keep, 0.0, -np.inf).astype(np.float32)
+    assert np.allclose(ref.sdpa(q[:, :2], k, v, mask=add), t, atol=1e-5)
+    # causal, top-left (is_causal) and bottom-right (torch's causal_lower_right bias)
+    kq = r.standard_normal((b, hkv, skv, d)).astype(np.float32)
+    t = F.scaled_dot_product_attention(_t(kq), _t(k), _t(v), is_causal=True).numpy()
+    assert np.allclose(ref.sdpa(kq, k, v, causal=1), t, atol=1e-5)
+    from torch.nn.attention.bias import causal_lower_right
+
+    qs = r.standard_normal((b, hkv, 5, d)).astype(np.float32)
+    t = F.scaled_dot_product_attention(_t(qs), _t(k), _t(v), attn_mask=causal_lower_right(5, skv)).numpy()
+    assert np.allclose(ref.sdpa(qs, k, v, causal=2), t, atol=1e-5)
+
+
+def test_sdpa_mask_closed_forms():
+    r = rng(11)
+    q, k, v = (r.standard_normal((3, 9, 4)).astype(np.float32) for _ in range(3))
+    base = ref.sdpa(q, k, v)
+    assert np.allclose(ref.sdpa(q, k, v, mask=np.zeros((9, 9), np.float32)), base, atol=1e-7)
+    # a constant added along a whole row changes nothing (shift invariance)
+    assert np.allclose(ref.sdpa(q, k, v, mask=np.full((9, 9), 7.5, np.float32)), base, atol=1e-5)
+    # only key 4 left: the output is V[4]
+    m = np.full((9, 9), -np.inf, np.float32)
+    m[:, 4] = 0
+    assert np.allclose(ref.sdpa(q, k, v, mask=m), np.broadcast_to(v[:, 4:5], (3, 9, 4)), atol=1e-7)
+    # causal: query 0 sees key 0 only
+    assert np.allclose(ref.sdpa(q, k, v, causal=1)[:, 0], v[:, 0], atol=1e-7)
+    # a row with every key masked is NaN; the other rows are untouched
+    m = np.zeros((9, 9), np.float32)
+    m[2] = -np.inf
+    out = ref.sdpa(q, k, v, mask=m)
+    assert np.isnan(out[:, 2]).all() and np.allclose(np.delete(out, 2, 1), np.delete(base, 2, 1), atol=1e-7)
+
+
 # ---- int8 -------------------------------------------------------------------------------
 
 
