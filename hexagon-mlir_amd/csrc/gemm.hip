@@ -1,6 +1,8 @@
 // GEMM dispatch: alignment checks, tile choice, and the element-wise kernel
-// used for operands the MFMA fast path cannot take (odd strides, K or N not a
-// multiple of 8, misaligned pointers).
+// used for operands the MFMA fast path cannot take (leading dimensions not a
+// multiple of 8, misaligned pointers).  Ragged N and K (not multiples of 8)
+// run on the MFMA path: ragged columns are stored element by element, and K
+// not a multiple of 8 runs the instantiations that mask the last K-step.
 #include "gemm_impl.h"
 
 namespace hxmi {
@@ -8,6 +10,7 @@ namespace gemm {
 hipError_t launch_fast_f16(int tile, bool nn, int epi, bool out_f32, bool rms, const KArgs& k, hipStream_t s);
 hipError_t launch_fast_bf16(int tile, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s);
 hipError_t launch_fast_w8(int tile, int epi, bool out_f32, const KArgs& k, hipStream_t s);
+hipError_t launch_fast_ragged(int tile, bool bf16, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s);
 
 namespace {
 
@@ -96,7 +99,9 @@ bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
 bool gemm_fast_path_ok(const GemmProblem& p) {
   const bool i8 = p.dtype == DT_W8A16;
-  if (p.K % (i8 ? 16 : 8) || p.N % (p.epilogue == EPI_SILU_MUL ? 32 : 8)) return false;
+  if (i8 && (p.K % 16 || p.N % 8)) return false;
+  if (p.epilogue == EPI_SILU_MUL && p.N % 32) return false;
+  if (p.K % 8 && p.rms) return false;  // the RMS prologue sums whole fragments
   if (p.lda % 8 || p.ldb % (i8 ? 16 : 8) || p.ldc % 8) return false;
   if (p.batch > 1 && (p.sA % 8 || p.sB % (i8 ? 16 : 8) || p.sC % 8)) return false;
   if (!gemm::aligned(p.A, 16) || !gemm::aligned(p.B, 16) || !gemm::aligned(p.C, 16)) return false;
@@ -155,6 +160,10 @@ namespace gemm {
 namespace {
 
 int tile_for(const GemmProblem& p) {
+  if (p.K % 8) {  // the ragged-K instantiations: 128x128 once its tiles cover the CUs
+    const int64_t t128 = ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch;
+    return t128 >= 256 ? TILE_128x128 : TILE_64x64;
+  }
   int tile = p.tile >= 0 ? p.tile : knob_or(KNOB_GEMM_TILE, -1);
   if (tile < 0 || tile >= TILE_COUNT) tile = gemm_pick_tile(p);
   if (p.epilogue == EPI_SILU_MUL && kTiles[tile].BN < 128) tile = TILE_64x128;
@@ -193,6 +202,7 @@ KArgs make_kargs(const GemmProblem& p, int tile) {
 
 hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream_t stream) {
   if ((int64_t)k.tiles_m * k.tiles_n * k.batch >= (1ll << 31)) return hipErrorInvalidValue;
+  if (p.K % 8) return launch_fast_ragged(tile, p.dtype == DT_BF16, !p.b_nt, p.epilogue, p.out_f32, k, stream);
   if (p.rms && p.dtype != DT_F16) return hipErrorNotSupported;
   if (p.dtype == DT_W8A16) return launch_fast_w8(tile, p.epilogue, p.out_f32, k, stream);
   if (p.dtype == DT_BF16) return launch_fast_bf16(tile, !p.b_nt, p.epilogue, p.out_f32, k, stream);
@@ -213,7 +223,7 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 // With int8 weights the slices run 64x64 tiles (Qwen2.5-0.5B down
 // projection at M = 256: 105 -> 128 TFLOP/s).
 int gemm_splits(const GemmProblem& p) {
-  if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || !gemm_fast_path_ok(p)) return 1;
+  if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || p.K % 8 || !gemm_fast_path_ok(p)) return 1;
   if (const int64_t e = knob(KNOB_SPLITK); e != KNOB_UNSET) return e < 1 ? 1 : (e > 16 ? 16 : (int)e);
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 127) / 128);
   if (tiles >= 384 || p.K < 3072) return 1;

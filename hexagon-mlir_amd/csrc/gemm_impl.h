@@ -147,7 +147,10 @@ __device__ __forceinline__ void store4(char* p, float v0, float v1, float v2, fl
 
 template <typename T>
 __device__ __forceinline__ void load_bias4(const char* bias, int n, int N, float* out) {
-  if (n < N) {
+  if (n + 4 > N) {  // ragged last columns
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = n + i < N ? (float)((const T*)bias)[n + i] : 0.f;
+  } else if (n < N) {
     short4v raw = *(const short4v*)(bias + (int64_t)n * 2);
     T t[4];
     __builtin_memcpy(t, &raw, 8);
@@ -176,6 +179,13 @@ __device__ __forceinline__ short8v dequant8(int2v raw) {
     o[2 * d + 1] = __builtin_bit_cast(half2v, hi) - bias;
   }
   return out;
+}
+
+// The first n (clamped to 0..8) of 8 packed 16-bit values, the rest zero.
+__device__ __forceinline__ short8v keep_first(short8v v, int n) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = e < n ? v[e] : (short)0;
+  return v;
 }
 
 template <typename F, int... Is>
@@ -240,7 +250,7 @@ __device__ __forceinline__ void pp_barrier() {
 // loads its next step's fragments from LDS and issues the global->LDS loads,
 // so every SIMD's MFMA pipe alternates between its two waves.
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool NN, typename T, int EPI, bool OUTF32,
-          bool BI8 = false, bool PP = false, bool RMS = false>
+          bool BI8 = false, bool PP = false, bool RMS = false, bool RAGGED = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -262,6 +272,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(!BI8 || (!NN && STAGES == 2 && BK == 64), "int8 B: [N,K], BK 64, 2 stages");
   static_assert(!PP || (NW == 8 && NWM == 2 && STAGES >= 3 && !BI8), "ping-pong: 2 x 4 waves, >= 3 stages");
   static_assert(!RMS || (!NN && !BI8 && !PP && !OUTF32 && sizeof(T) == 2), "RMSNorm prologue: NT fp16, standard schedule");
+  static_assert(!RAGGED || (!BI8 && !PP && !RMS), "ragged K: plain fp16 / bf16 operands, standard schedule");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int lane = threadIdx.x & 63;
@@ -386,7 +397,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     lofA[s] = (uint32_t)(wm * WM * RB) + o;
     lofB[s] = (uint32_t)(wn * WN * RB) + o;
   }
-  auto read_frags = [&](short8v (&fa)[TM], short8v (&fb)[TN], const char* sA_, const char* sB_, int s) {
+  // RAGGED (K % 8 != 0): the 16-byte chunk that straddles K brings in
+  // elements past K (row padding, or the next row).  In the last K-step the
+  // fragments keep only their elements below K; the NN B operand needs no
+  // mask, its rows past K read as zero.
+  auto read_frags = [&](short8v (&fa)[TM], short8v (&fb)[TN], const char* sA_, const char* sB_, int s,
+                        int kstep) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
       if constexpr (NN)
@@ -396,6 +412,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     }
 #pragma unroll
     for (int j = 0; j < TM; ++j) fa[j] = *(const short8v*)(sA_ + lofA[s] + j * 32 * RB);
+    if constexpr (RAGGED) {
+      if (kstep == nk - 1) {
+        const int nv = K - (kstep * BK + s * 16 + (lane >> 5) * 8);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) fa[j] = keep_first(fa[j], nv);
+        if constexpr (!NN) {
+#pragma unroll
+          for (int i = 0; i < TN; ++i) fb[i] = keep_first(fb[i], nv);
+        }
+      }
+    }
   };
 
   float16v acc[TN][TM];
@@ -441,7 +468,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       issue(kt + D, stw);
       const char* sA_ = smem + st * STAGE;
       const char* sB_ = sA_ + A_BYTES;
-      static_for<SUBS>([&](auto S) { read_frags(fa[decltype(S)::value], fb[decltype(S)::value], sA_, sB_, decltype(S)::value); });
+      static_for<SUBS>([&](auto S) { read_frags(fa[decltype(S)::value], fb[decltype(S)::value], sA_, sB_, decltype(S)::value, kt); });
       wait_vmcnt<(D - 1) * NVM>();
       pp_barrier();
       static_for<SUBS>([&](auto S) {
@@ -467,7 +494,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   wait_vmcnt<(STAGES - 1) * NVM>();
   __syncthreads();
   short8v fa[2][TM], fb[2][TN];
-  read_frags(fa[0], fb[0], smem, smem + A_BYTES, 0);
+  read_frags(fa[0], fb[0], smem, smem + A_BYTES, 0, 0);
   int st = 0;
   for (int kt = 0; kt < nk; ++kt) {
     const int st1 = (st + 1 == STAGES) ? 0 : st + 1;
@@ -477,14 +504,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       constexpr int s = decltype(S)::value;
       constexpr int nxt = (s + 1) & 1;
       if constexpr (s + 1 < SUBS) {
-        read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1);
+        read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1, kt);
         if constexpr (BI8 && s == 1) store_q(st1);
       } else {
         wait_vmcnt<(STAGES - 2) * NVM>();
         __syncthreads();
         // fragment reads first, then the refill loads: the same order as the
         // schedule below, so the loads can be spread between the MFMAs
-        read_frags(fa[nxt], fb[nxt], smem + st1 * STAGE, smem + st1 * STAGE + A_BYTES, 0);
+        read_frags(fa[nxt], fb[nxt], smem + st1 * STAGE, smem + st1 * STAGE + A_BYTES, 0, kt + 1);
         issue(kt + STAGES, st);
         if constexpr (BI8) load_q(kt + 2);
       }
@@ -658,8 +685,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = gelu_tanh(v[q]);
           }
-          if (m < a.M && n < a.N)
+          if (m < a.M && n + 4 <= a.N) {
             *(float4v*)(Cb + ((int64_t)m * a.ldc + n) * 4) = float4v{v[0], v[1], v[2], v[3]};
+          } else if (m < a.M && n < a.N) {  // ragged last columns
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (n + q < a.N) ((float*)Cb)[(int64_t)m * a.ldc + n + q] = v[q];
+          }
         }
       }
     return;
@@ -721,9 +753,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     for (int t = threadIdx.x; t < BM * CPRO; t += NT) {
       const int row = t / CPRO, cc = t % CPRO;
       const int m = m0 + row, n = n0o + cc * 8;
-      if (m < a.M && n < Nout) {
+      if (m < a.M && n + 8 <= Nout) {
         int4v v = *(const int4v*)(smem + row * SROW + cc * 16);
         *(int4v*)(Cb + ((int64_t)m * a.ldc + n) * 2) = v;
+      } else if (m < a.M && n < Nout) {  // ragged last columns
+        const short* src = (const short*)(smem + row * SROW + cc * 16);
+        short* dst = (short*)(Cb + ((int64_t)m * a.ldc + n) * 2);
+        for (int q = 0; q < Nout - n; ++q) dst[q] = src[q];
       }
     }
   }
@@ -757,13 +793,13 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {128, 128, 32, 64, 64, 2},         // TILE_128x128_W8
 };
 
-template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false>
+template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false, bool RAGGED = false>
 hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr TileShape s = kTiles[TILE];
   constexpr int threads = (s.BM / s.WM) * (s.BN / s.WN) * 64;
   const int64_t blocks = (int64_t)k.tiles_m * k.tiles_n * k.batch;
   hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8,
-                                (s.PP && !BI8 && !RMS), RMS>),
+                                (s.PP && !BI8 && !RMS), RMS, RAGGED>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
 }

@@ -68,16 +68,36 @@ __device__ __forceinline__ short4v lds_read_tr16(const char* p) {
   return __builtin_bit_cast(short4v, v);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// Wave reductions without LDS round trips: DPP swaps inside each row of 16
+// lanes (quad permutes, then rotations by 4 and 8 that cover the row), then
+// v_permlane16_swap / v_permlane32_swap across rows.  Every lane receives
+// the result.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce_dpp(float v, Op op) {
+  auto dpp = [](float x, int ctrl) {
+    switch (ctrl) {  // the control word must be a constant
+      case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+      case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+      case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));
+      default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+    }
+  };
+  v = op(v, dpp(v, 0));  // quad_perm [1,0,3,2]
+  v = op(v, dpp(v, 1));  // quad_perm [2,3,0,1]
+  v = op(v, dpp(v, 2));  // row_ror:4
+  v = op(v, dpp(v, 3));  // row_ror:8
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  return wave_reduce_dpp(v, [](float x, float y) { return fmaxf(x, y); });
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  return wave_reduce_dpp(v, [](float x, float y) { return x + y; });
 }
 
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void rmsnorm_vec(RArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float r = __builtin_amdgcn_rsqf(ss / (float)a.cols + a.eps);
   char* yrow = a.y + row * a.ldy * 2;
 #pragma unroll
@@ -98,14 +98,19 @@ __global__ __launch_bounds__(256) void rmsnorm_any(RArgs a) {
     const float f = (float)x[c];
     ss += f * f;
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float r = __builtin_amdgcn_rsqf(ss / (float)a.cols + a.eps);
   for (int c = lane; c < a.cols; c += 64) y[c] = (T)((float)g[c] * (float)(T)((float)x[c] * r));
 }
 
 // ---- softmax: y = exp(s*x - max) / sum ---------------------------------------
 
-// EPL elements per lane, strided by 64 (coalesced 2-byte loads; any alignment).
+// EPL elements per lane, strided by 64 (coalesced 2-byte loads; any
+// alignment).  The max and the sum go through DPP and lane-swap reductions
+// (no LDS round trip): softmax [18912, 197] 7.07 -> 6.27 us on one MI355X.
+// Several rows per wave, all loads issued first, measured slower (2 rows
+// 6.57 us, 4 rows 7.75 us), as did staging blocks of rows through LDS with
+// 16-byte global accesses (11-15 us).
 template <typename T, int EPL>
 __global__ __launch_bounds__(256) void softmax_reg(RArgs a) {
   const int lane = threadIdx.x & 63;
@@ -121,7 +126,7 @@ __global__ __launch_bounds__(256) void softmax_reg(RArgs a) {
     v[i] = c < a.cols ? (float)x[c] * a.scale : -INFINITY;
     mx = fmaxf(mx, v[i]);
   }
-  mx = wave_max(mx);
+  mx = wave_max_dpp(mx);
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(256) void softmax_reg(RArgs a) {
     v[i] = c < a.cols ? fast_exp(v[i] - mx) : 0.f;
     sum += v[i];
   }
-  sum = wave_sum(sum);
+  sum = wave_sum_dpp(sum);
   const float inv = 1.0f / sum;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -148,10 +153,10 @@ __global__ __launch_bounds__(256) void softmax_any(RArgs a) {
   T* y = (T*)a.y + row * a.ldy;
   float mx = -INFINITY;
   for (int c = lane; c < a.cols; c += 64) mx = fmaxf(mx, (float)x[c] * a.scale);
-  mx = wave_max(mx);
+  mx = wave_max_dpp(mx);
   float sum = 0.f;
   for (int c = lane; c < a.cols; c += 64) sum += fast_exp((float)x[c] * a.scale - mx);
-  sum = wave_sum(sum);
+  sum = wave_sum_dpp(sum);
   const float inv = 1.0f / sum;
   for (int c = lane; c < a.cols; c += 64) y[c] = (T)(fast_exp((float)x[c] * a.scale - mx) * inv);
 }

@@ -549,8 +549,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional
     if mask is not None or causal or group != 1:
         raise HxmiError("masked, causal and grouped-query attention run on the fused kernel only "
                         "(fp16, head dim 64 or 128, scale > 0)")
-    s = bgemm(q3, k3, b_layout="nt", alpha=scale)
-    p = softmax(s)
+    # S and P rows padded to a multiple of 8 keys, so both GEMMs (ragged N
+    # for Q.K^T, ragged K for P.V) run on the MFMA path; softmax in place
+    skv8 = (Skv + 7) // 8 * 8
+    sbuf = torch.empty((q3.shape[0], S, skv8), dtype=q.dtype, device=q.device)
+    s = bgemm(q3, k3, b_layout="nt", alpha=scale, out=sbuf[..., :Skv])
+    p = softmax(s, out=s)
     if out is not None:
         bgemm(p, v3, b_layout="nn", out=out.view(-1, S, v.shape[-1]))
         return out

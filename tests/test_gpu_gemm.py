@@ -71,6 +71,89 @@ def test_gemm_unaligned_elementwise_path(pkg, dev, layout, M, N, K, lda):
     assert ref.max_rel_err(np32(c.cpu()), ref.matmul(a.numpy(), b.numpy(), layout)) <= TOL
 
 
+def _nan_padded(t, cols):
+    """t as the leading columns of a wider buffer whose other columns are NaN:
+    any read of them that reaches a result shows up as NaN."""
+    full = torch.full((t.shape[0], cols), float("nan"), dtype=t.dtype)
+    full[:, : t.shape[1]] = t
+    return full
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("M,N,K", [(5, 24, 1), (33, 40, 3), (64, 72, 13), (130, 264, 197), (300, 136, 517),
+                                   (1024, 1024, 999), (197, 197, 197), (7, 9, 11)])
+def test_gemm_ragged_k_and_n_on_mfma(pkg, dev, layout, M, N, K):
+    """K and N not multiples of 8 on the MFMA path: operands are views of
+    NaN-padded buffers (leading dims rounded up to 8), so an element past K
+    that reaches a sum, or a store past N, is caught."""
+    k8, n8 = (K + 7) // 8 * 8, (N + 7) // 8 * 8
+    a = uniform((M, K), 31)
+    b = uniform((K, N) if layout == "nn" else (N, K), 32)
+    ap = _nan_padded(a, k8).to(dev)
+    bp = (_nan_padded(b, n8) if layout == "nn" else _nan_padded(b, k8)).to(dev)
+    outp = torch.full((M, n8), 7.0, dtype=torch.float16, device=dev)
+    pkg.gemm(ap[:, :K], bp[:, : b.shape[1]], b_layout=layout, out=outp[:, :N])
+    torch.cuda.synchronize()
+    c = outp.cpu()
+    assert ref.max_rel_err(np32(c[:, :N]), ref.matmul(a.numpy(), b.numpy(), layout)) <= TOL
+    assert (c[:, N:] == 7.0).all()  # padding columns untouched
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("K", [1, 5, 197])
+def test_gemm_ragged_k_exact_integer(pkg, dev, layout, K):
+    """Small integers give exact fp32 sums: the ragged-K path must return the
+    exactly rounded products bit for bit."""
+    g = torch.Generator().manual_seed(33)
+    M, N = 130, 72
+    a = torch.randint(-4, 5, (M, K), generator=g).half()
+    b = torch.randint(-4, 5, (K, N) if layout == "nn" else (N, K), generator=g).half()
+    k8 = (K + 7) // 8 * 8
+    ap = _nan_padded(a, k8).to(dev)
+    bp = b.to(dev) if layout == "nn" else _nan_padded(b, k8).to(dev)
+    c = pkg.gemm(ap[:, :K], bp if layout == "nn" else bp[:, :K], b_layout=layout)
+    torch.cuda.synchronize()
+    exact = a.double() @ (b.double() if layout == "nn" else b.double().T)
+    assert np.array_equal(c.cpu().numpy(), f16_round(exact.numpy()))
+
+
+@pytest.mark.parametrize("epi", ["bias", "gelu_tanh", "bias_gelu_tanh", "silu_mul"])
+def test_gemm_ragged_k_epilogues(pkg, dev, epi):
+    M, N, K = 200, 96 if epi == "silu_mul" else 93, 301
+    x = normal((M, K), 34)
+    w = normal((N, K), 35, std=0.05)
+    bias = normal((N,), 36, std=0.1)
+    xp, wp = _nan_padded(x, 304).to(dev), _nan_padded(w, 304).to(dev)
+    n_out = N // 2 if epi == "silu_mul" else N
+    outp = torch.empty((M, 104), dtype=torch.float16, device=dev)
+    kw = {"bias": bias.to(dev)} if "bias" in epi else {}
+    pkg.gemm(xp[:, :K], wp[:, :K], b_layout="nt", epilogue=epi, out=outp[:, :n_out], **kw)
+    torch.cuda.synchronize()
+    exp = ref.gemm_epilogue(x.numpy(), w.numpy(), "nt", epi, bias.numpy() if "bias" in epi else None)
+    assert ref.max_rel_err(np32(outp[:, :n_out].cpu()), exp) <= TOL
+
+
+def test_gemm_ragged_bf16(pkg, dev):
+    M, N, K = 150, 77, 123
+    a = uniform((M, K), 37, dtype=torch.bfloat16)
+    b = uniform((N, K), 38, dtype=torch.bfloat16)
+    ap, bp = _nan_padded(a, 128).to(dev), _nan_padded(b, 128).to(dev)
+    outp = torch.empty((M, 80), dtype=torch.bfloat16, device=dev)
+    pkg.gemm(ap[:, :K], bp[:, :K], b_layout="nt", out=outp[:, :N])
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(outp[:, :N].cpu()), ref.matmul(np32(a), np32(b), "nt")) <= TOL
+
+
+def test_composite_attention_runs_the_mfma_gemms(pkg, dev):
+    """Head dim 80 takes the reference's three steps (Q.K^T, softmax, P.V)
+    with S and P padded to 200 keys: both GEMMs on the MFMA path."""
+    q, k, v = (normal((24, 197, 80), 39 + i) for i in range(3))
+    o = pkg.attention(q.to(dev), k.to(dev), v.to(dev), 80**-0.5)
+    torch.cuda.synchronize()
+    exp = ref.sdpa(q.numpy(), k.numpy(), v.numpy(), 80**-0.5)
+    assert ref.max_err_vs_scale(np32(o.cpu()), exp) <= TOL
+
+
 @pytest.mark.parametrize("epi", ["bias", "gelu_tanh", "bias_gelu_tanh"])
 @pytest.mark.parametrize("tile", [None, 0, 3, 6, 7, 8, 9, 10, 11, 12, 13])
 def test_gemm_epilogues(pkg, dev, force_tile, epi, tile):
