@@ -258,7 +258,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   constexpr int CH = RB / 16;           // 16-byte chunks per row
   constexpr int RPIK = 1024 / RB;       // k-contiguous rows per 1 KB wave instruction
   constexpr int A_BYTES = BM * RB;
-  constexpr int B_BYTES = BN * RB;
+  constexpr int B_BYTES = BI8 ? BN * BK : BN * RB;  // int8 B stays int8 in LDS
   constexpr int STAGE = A_BYTES + B_BYTES;
   constexpr int BNO = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int SROW = BNO * 2 + 16;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(SMEM <= 160 * 1024, "LDS budget");
   static_assert(BM % (RPIK * NW) == 0, "A tile rows per wave");
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
-  static_assert(!BI8 || (!NN && STAGES == 2 && BK == 64), "int8 B: [N,K], BK 64, 2 stages");
+  static_assert(!BI8 || (!NN && BK == 64 && BN % (16 * NW) == 0), "int8 B: [N,K], BK 64, 16-row loads");
   static_assert(!PP || (NW == 8 && NWM == 2 && STAGES >= 3 && !BI8), "ping-pong: 2 x 4 waves, >= 3 stages");
   static_assert(!RMS || (!NN && !BI8 && !PP && !OUTF32 && sizeof(T) == 2), "RMSNorm prologue: NT fp16, standard schedule");
   static_assert(!RAGGED || (!BI8 && !PP && !RMS), "ragged K: plain fp16 / bf16 operands, standard schedule");
@@ -309,53 +309,32 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 
   constexpr int CPR = BN / 8;                          // NN: 16-byte chunks per k-row
   constexpr int RPI = NN ? (1024 / (BN * 2)) : RPIK;   // rows per wave instruction
-  constexpr int IB = BI8 ? 1 : (NN ? (BK / RPI / NW) : (BN / RPIK / NW));
+  // int8 B (BI8): 64-byte rows (BK int8 weights), four 16-byte chunks per
+  // row, one 1 KB instruction per 16 rows; chunk c of row r is stored at
+  // position c ^ ((r >> 2) & 3), which depends on the lane alone (rows of an
+  // instruction start on multiples of 16).
+  constexpr int IB = BI8 ? BN / 16 / NW : (NN ? (BK / RPI / NW) : (BN / RPIK / NW));
   static_assert(IB >= 1, "B load plan");
   static_assert(!NN || (NW * RPI) % 4 == 0, "NN swizzle period");
   uint32_t voffB, stepB, bytesB;
+  int cB8 = 0;
   if constexpr (NN) {
     const int rowl = w * RPI + lane / CPR;  // (row & 3) is the same for every instruction
     const int c = (lane % CPR) ^ nn_swz<BN>(rowl);
     voffB = (n0 + c * 8) < a.N ? (uint32_t)(rowl * a.ldb * 2 + c * 16) : kOOB;
     stepB = (uint32_t)(NW * RPI * a.ldb * 2);
     bytesB = (uint32_t)(a.ldb * 2);  // per valid k-row
+  } else if constexpr (BI8) {
+    cB8 = (lane & 3) ^ ((lane >> 4) & 3);
+    voffB = (uint32_t)((w * 16 + (lane >> 2)) * a.ldb + cB8 * 16);
+    stepB = (uint32_t)(NW * 16 * a.ldb);
+    bytesB = (uint32_t)(min(BN, a.N - n0) * a.ldb);
   } else {
-    voffB = (uint32_t)((w * RPIK + lane / CH) * a.ldb * (BI8 ? 1 : 2) + cA * 16);
+    voffB = (uint32_t)((w * RPIK + lane / CH) * a.ldb * 2 + cA * 16);
     stepB = (uint32_t)(NW * RPIK * a.ldb * 2);
-    bytesB = (uint32_t)(min(BN, a.N - n0) * a.ldb * (BI8 ? 1 : 2));
+    bytesB = (uint32_t)(min(BN, a.N - n0) * a.ldb * 2);
   }
   const int nk = (K + BK - 1) / BK;
-
-  // int8 B: register-staged, 16 weights (one row, 16 k) per 16-byte load,
-  // dequantised to fp16 on the way into the same swizzled LDS layout.
-  constexpr int I8L = BI8 ? (BN * 4 + NT - 1) / NT : 1;
-  int4v regQ[I8L];
-  auto load_q = [&](int kt) {
-    const int k0 = kt * BK;
-    const uint32_t nr = kt < nk ? bytesB - (uint32_t)k0 : 0u;
-    const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Bb + k0, nr);
-#pragma unroll
-    for (int i = 0; i < I8L; ++i) {
-      const int idx = i * NT + threadIdx.x;
-      const int r = idx >> 2, q = idx & 3;
-      const bool ok = idx < BN * 4 && (k0 + q * 16) < K;
-      regQ[i] = load16(rQ, ok ? (uint32_t)(r * a.ldb + q * 16) : kOOB);
-    }
-  };
-  auto store_q = [&](int stage) {
-    char* sB_ = smem + stage * STAGE + A_BYTES;
-#pragma unroll
-    for (int i = 0; i < I8L; ++i) {
-      const int idx = i * NT + threadIdx.x;
-      if (BN * 4 % NT == 0 || idx < BN * 4) {
-        const int r = idx >> 2, q = idx & 3;
-        const short8v lo = dequant8(int2v{regQ[i][0], regQ[i][1]});
-        const short8v hi = dequant8(int2v{regQ[i][2], regQ[i][3]});
-        *(short8v*)(sB_ + r * RB + (((2 * q) ^ kc_swz<RB>(r)) << 4)) = lo;
-        *(short8v*)(sB_ + r * RB + (((2 * q + 1) ^ kc_swz<RB>(r)) << 4)) = hi;
-      }
-    }
-  };
 
   // Loads of K-step kt into LDS stage `stage`; a step past the end issues
   // loads against an empty buffer (all zeros, nothing touched).
@@ -375,7 +354,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
       for (int i = 0; i < IB; ++i)
         load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + (i * NW + w) * 1024), voffB + i * stepB);
-    } else if constexpr (!BI8) {
+    } else if constexpr (BI8) {
+      const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + k0, live ? bytesB - (uint32_t)k0 : 0u);
+      const uint32_t vB = (k0 + cB8 * 16) < K ? voffB : kOOB;
+#pragma unroll
+      for (int i = 0; i < IB; ++i)
+        load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + (i * NW + w) * 1024), vB + i * stepB);
+    } else {
       const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + (int64_t)k0 * 2, live ? bytesB - 2u * k0 : 0u);
       const uint32_t vB = (k0 + cA * 8) < K ? voffB : kOOB;
 #pragma unroll
@@ -405,10 +390,15 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
                         int kstep) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
-      if constexpr (NN)
+      if constexpr (NN) {
         fb[i] = read_nn<BN>(sB_, wn * WN + i * 32, s, lane);
-      else
+      } else if constexpr (BI8) {
+        // 8 int8 weights (row r, k = 16 s + 8 (lane / 32) ..) -> 8 fp16, exactly
+        const int r = wn * WN + i * 32 + (lane & 31);
+        fb[i] = dequant8(*(const int2v*)(sB_ + r * BK + ((s ^ ((r >> 2) & 3)) << 4) + (lane >> 5) * 8));
+      } else {
         fb[i] = *(const short8v*)(sB_ + lofB[s] + i * 32 * RB);
+      }
     }
 #pragma unroll
     for (int j = 0; j < TM; ++j) fa[j] = *(const short8v*)(sA_ + lofA[s] + j * 32 * RB);
@@ -444,7 +434,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   //   step's global loads in between.
   constexpr int SUBS = BK / 16;
   constexpr int NDS = (NN ? 2 * TN : TN) + TM;  // LDS read instructions per substep
-  constexpr int NVM = BI8 ? IA : IA + IB;       // global->LDS loads per K-step per wave
+  constexpr int NVM = IA + IB;                  // global->LDS loads per K-step per wave
   if constexpr (PP) {
     // Phases alternate memory / compute; group 0 runs phase 2k as the memory
     // phase of step k and 2k+1 as its compute phase, group 1 one phase later.
@@ -486,11 +476,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   } else {
 #pragma unroll
   for (int p = 0; p < STAGES; ++p) issue(p, p);
-  if constexpr (BI8) {
-    load_q(0);
-    store_q(0);
-    load_q(1);
-  }
   wait_vmcnt<(STAGES - 1) * NVM>();
   __syncthreads();
   short8v fa[2][TM], fb[2][TN];
@@ -505,7 +490,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       constexpr int nxt = (s + 1) & 1;
       if constexpr (s + 1 < SUBS) {
         read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1, kt);
-        if constexpr (BI8 && s == 1) store_q(st1);
       } else {
         wait_vmcnt<(STAGES - 2) * NVM>();
         __syncthreads();
@@ -513,7 +497,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
         // schedule below, so the loads can be spread between the MFMAs
         read_frags(fa[nxt], fb[nxt], smem + st1 * STAGE, smem + st1 * STAGE + A_BYTES, 0, kt + 1);
         issue(kt + STAGES, st);
-        if constexpr (BI8) load_q(kt + 2);
       }
 #pragma unroll
       for (int i = 0; i < TN; ++i)
@@ -798,7 +781,11 @@ hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr TileShape s = kTiles[TILE];
   constexpr int threads = (s.BM / s.WM) * (s.BN / s.WN) * 64;
   const int64_t blocks = (int64_t)k.tiles_m * k.tiles_n * k.batch;
-  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8,
+  // int8 B: BK 64, and three LDS stages where they fit (the weights stream
+  // from HBM, so the deeper prefetch pays)
+  constexpr int W8_STAGE = s.BM * 128 + s.BN * 64;
+  constexpr int W8_STAGES = 3 * W8_STAGE <= 160 * 1024 ? 3 : 2;
+  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? W8_STAGES : s.STAGES), NN, T, EPI, OUTF32, BI8,
                                 (s.PP && !BI8 && !RMS), RMS, RAGGED>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
