@@ -225,9 +225,10 @@ int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int
                      epilogue, alpha, 0, nullptr, 0, stream, "hxmi_bgemm_bf16");
 }
 
-int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                  int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream) {
-  const char* name = "hxmi_gemv_f16";
+namespace {
+int gemv_common(int dtype, const char* name, const void* x, const void* W, const void* bias, void* y, int64_t M,
+                int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", name);
   if (M == 0 || N == 0) return ok();
   REQUIRE(x && W && y, "%s: null pointer", name);
@@ -236,7 +237,7 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
                        al(x, 16) && al(W, 16) && al(y, 8) && (!bias || al(bias, 8)) && 64 * ldw * 2 < (1ll << 31) &&
                        16 * ldx * 2 < (1ll << 31);
   if (!gemv_ok)
-    return gemm_common(hxmi::DT_F16, x, W, y, bias, 1, M, N, K, ldx, ldw, ldy, 0, 0, 0, 1,
+    return gemm_common(dtype, x, W, y, bias, 1, M, N, K, ldx, ldw, ldy, 0, 0, 0, 1,
                        bias ? HXMI_EPI_BIAS : HXMI_EPI_NONE, 1.f, 0, nullptr, 0, stream, name);
   hxmi::GemvProblem p{};
   p.x = x;
@@ -250,9 +251,23 @@ int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64
   p.ldw = ldw;
   p.ldy = ldy;
   p.w_int8 = 0;
+  p.dtype = dtype;
   p.ws = workspace_bytes > 0 ? workspace : nullptr;
   p.ws_bytes = workspace_bytes > 0 ? workspace_bytes : 0;
   return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
+}
+}  // namespace
+
+int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                  int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemv_common(hxmi::DT_F16, "hxmi_gemv_f16", x, W, bias, y, M, N, K, ldx, ldw, ldy, workspace,
+                     workspace_bytes, stream);
+}
+
+int hxmi_gemv_bf16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                   int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemv_common(hxmi::DT_BF16, "hxmi_gemv_bf16", x, W, bias, y, M, N, K, ldx, ldw, ldy, workspace,
+                     workspace_bytes, stream);
 }
 
 int64_t hxmi_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
@@ -413,30 +428,54 @@ int hxmi_attention_f16(const void* q, const void* k, const void* v, void* o, int
                           stride_v, stride_o, 1, nullptr, 0, 0, 1, 0, scale, stream);
 }
 
-int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
-                            int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
-                            const float* rscale_in, void* stream) {
-  const char* name = "hxmi_rmsnorm_linear_f16";
+namespace {
+int rms_linear_common(int dtype, const char* name, const void* x, const void* Wg, void* C, const void* bias, int64_t M,
+                      int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps,
+                      float* rscale_out, const float* rscale_in, void* stream) {
   REQUIRE(epilogue == HXMI_EPI_NONE || epilogue == HXMI_EPI_BIAS || epilogue == HXMI_EPI_SILU_MUL,
           "%s: epilogue %d unsupported (none, bias or silu_mul)", name, epilogue);
   REQUIRE(K > 0 || M <= 0 || N <= 0, "%s: RMSNorm over zero columns", name);
   REQUIRE(eps >= 0.f, "%s: negative eps", name);
   REQUIRE(!(rscale_out && rscale_in), "%s: rscale_out and rscale_in are exclusive", name);
   if (rscale_in)  // statistics given: a plain GEMM with a row scale before the epilogue
-    return gemm_common(hxmi::DT_F16, x, Wg, C, bias, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0,
-                       nullptr, 0, stream, name, 0, 0.f, nullptr, rscale_in);
-  return gemm_common(hxmi::DT_F16, x, Wg, C, bias, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr,
-                     0, stream, name, 1, eps, rscale_out, nullptr);
+    return gemm_common(dtype, x, Wg, C, bias, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr, 0,
+                       stream, name, 0, 0.f, nullptr, rscale_in);
+  return gemm_common(dtype, x, Wg, C, bias, 1, M, N, K, ldx, ldw, ldc, 0, 0, 0, 1, epilogue, 1.f, 0, nullptr, 0,
+                     stream, name, 1, eps, rscale_out, nullptr);
 }
 
-int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
-                                 int64_t ldwg, void* stream) {
-  const char* name = "hxmi_fold_rmsnorm_weight_f16";
+int fold_common(int dtype, const char* name, const void* W, const void* g, void* Wg, int64_t N, int64_t K,
+                int64_t ldw, int64_t ldwg, void* stream) {
   REQUIRE(N >= 0 && K >= 0, "%s: negative size", name);
   if (N == 0 || K == 0) return ok();
   REQUIRE(W && g && Wg, "%s: null pointer", name);
   REQUIRE(ldw >= K && ldwg >= K, "%s: leading dimension smaller than K", name);
-  return from_hip(hxmi::launch_fold_rms_weight(W, g, Wg, N, K, ldw, ldwg, (hipStream_t)stream), name);
+  return from_hip(hxmi::launch_fold_rms_weight(dtype, W, g, Wg, N, K, ldw, ldwg, (hipStream_t)stream), name);
+}
+}  // namespace
+
+int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N, int64_t K,
+                            int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
+                            const float* rscale_in, void* stream) {
+  return rms_linear_common(hxmi::DT_F16, "hxmi_rmsnorm_linear_f16", x, Wg, C, bias, M, N, K, ldx, ldw, ldc, epilogue,
+                           eps, rscale_out, rscale_in, stream);
+}
+
+int hxmi_rmsnorm_linear_bf16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N,
+                             int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps,
+                             float* rscale_out, const float* rscale_in, void* stream) {
+  return rms_linear_common(hxmi::DT_BF16, "hxmi_rmsnorm_linear_bf16", x, Wg, C, bias, M, N, K, ldx, ldw, ldc,
+                           epilogue, eps, rscale_out, rscale_in, stream);
+}
+
+int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+                                 int64_t ldwg, void* stream) {
+  return fold_common(hxmi::DT_F16, "hxmi_fold_rmsnorm_weight_f16", W, g, Wg, N, K, ldw, ldwg, stream);
+}
+
+int hxmi_fold_rmsnorm_weight_bf16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+                                  int64_t ldwg, void* stream) {
+  return fold_common(hxmi::DT_BF16, "hxmi_fold_rmsnorm_weight_bf16", W, g, Wg, N, K, ldw, ldwg, stream);
 }
 
 int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, int64_t K, int64_t ldw, int64_t ldq,

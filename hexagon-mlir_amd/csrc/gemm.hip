@@ -8,7 +8,7 @@
 namespace hxmi {
 namespace gemm {
 hipError_t launch_fast_f16(int tile, bool nn, int epi, bool out_f32, bool rms, const KArgs& k, hipStream_t s);
-hipError_t launch_fast_bf16(int tile, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s);
+hipError_t launch_fast_bf16(int tile, bool nn, int epi, bool out_f32, bool rms, const KArgs& k, hipStream_t s);
 hipError_t launch_fast_w8(int tile, int epi, bool out_f32, const KArgs& k, hipStream_t s);
 hipError_t launch_fast_ragged(int tile, bool bf16, bool nn, int epi, bool out_f32, const KArgs& k, hipStream_t s);
 
@@ -203,9 +203,9 @@ KArgs make_kargs(const GemmProblem& p, int tile) {
 hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream_t stream) {
   if ((int64_t)k.tiles_m * k.tiles_n * k.batch >= (1ll << 31)) return hipErrorInvalidValue;
   if (p.K % 8) return launch_fast_ragged(tile, p.dtype == DT_BF16, !p.b_nt, p.epilogue, p.out_f32, k, stream);
-  if (p.rms && p.dtype != DT_F16) return hipErrorNotSupported;
+  if (p.rms && p.dtype == DT_W8A16) return hipErrorNotSupported;
   if (p.dtype == DT_W8A16) return launch_fast_w8(tile, p.epilogue, p.out_f32, k, stream);
-  if (p.dtype == DT_BF16) return launch_fast_bf16(tile, !p.b_nt, p.epilogue, p.out_f32, k, stream);
+  if (p.dtype == DT_BF16) return launch_fast_bf16(tile, !p.b_nt, p.epilogue, p.out_f32, p.rms != 0, k, stream);
   return launch_fast_f16(tile, !p.b_nt, p.epilogue, p.out_f32, p.rms != 0, k, stream);
 }
 

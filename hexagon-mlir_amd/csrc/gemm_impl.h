@@ -18,6 +18,7 @@
 //     SiLU-mul, tanh-GELU) and the LDS-staged 16-byte stores cheap.
 #pragma once
 
+#include <type_traits>
 #include <utility>
 
 #include "hxmi_common.h"
@@ -181,6 +182,27 @@ __device__ __forceinline__ short8v dequant8(int2v raw) {
   return out;
 }
 
+// ss + the sum of squares of 8 packed fp16 / bf16 values (v_dot2 on pairs).
+template <typename T>
+__device__ __forceinline__ float sumsq8(short8v v, float ss) {
+  if constexpr (std::is_same_v<T, _Float16>) {
+    const half8v h = __builtin_bit_cast(half8v, v);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const half2v p2 = {h[2 * q], h[2 * q + 1]};
+      ss = __builtin_amdgcn_fdot2(p2, p2, ss, false);
+    }
+  } else {
+    const bf16x8v h = __builtin_bit_cast(bf16x8v, v);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bf16x2v p2 = {h[2 * q], h[2 * q + 1]};
+      ss = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, ss, false);
+    }
+  }
+  return ss;
+}
+
 // The first n (clamped to 0..8) of 8 packed 16-bit values, the rest zero.
 __device__ __forceinline__ short8v keep_first(short8v v, int n) {
 #pragma unroll
@@ -271,7 +293,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
   static_assert(!BI8 || (!NN && BK == 64 && BN % (16 * NW) == 0), "int8 B: [N,K], BK 64, 16-row loads");
   static_assert(!PP || (NW == 8 && NWM == 2 && STAGES >= 3 && !BI8), "ping-pong: 2 x 4 waves, >= 3 stages");
-  static_assert(!RMS || (!NN && !BI8 && !PP && !OUTF32 && sizeof(T) == 2), "RMSNorm prologue: NT fp16, standard schedule");
+  static_assert(!RMS || (!NN && !BI8 && !PP && !OUTF32), "RMSNorm prologue: NT, standard schedule");
   static_assert(!RAGGED || (!BI8 && !PP && !RMS), "ragged K: plain fp16 / bf16 operands, standard schedule");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
@@ -504,14 +526,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
         for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[s & 1][i], fa[s & 1][j], acc[i][j]);
       if constexpr (RMS) {
 #pragma unroll
-        for (int j = 0; j < TM; ++j) {
-          const half8v h = __builtin_bit_cast(half8v, fa[s & 1][j]);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const half2v p2 = {h[2 * q], h[2 * q + 1]};
-            ss[j] = __builtin_amdgcn_fdot2(p2, p2, ss[j], false);
-          }
-        }
+        for (int j = 0; j < TM; ++j) ss[j] = sumsq8<T>(fa[s & 1][j], ss[j]);
       }
       schedule_substep<TN * TM, NDS, (s + 1 < SUBS) ? 0 : NVM, RMS ? TM * 4 : 0>();
       __builtin_amdgcn_sched_barrier(0);

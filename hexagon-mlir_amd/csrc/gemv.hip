@@ -22,6 +22,8 @@
 //   * gemv_pair_ks: K > 1024 on at most 2048 rows (down projections), the
 //     same loads with K split over one workgroup's waves;
 //   * gemv_valu: M <= 8 on other long matrices, on the vector ALUs.
+#include <type_traits>
+
 #include "hxmi_common.h"
 #include "hxmi_internal.h"
 
@@ -46,10 +48,32 @@ struct VArgs {
 
 typedef float float2v __attribute__((ext_vector_type(2)));
 
+// 16x16x32 MFMA on fp16 or bf16 operands (T).
+template <typename T>
 __device__ __forceinline__ float4v mfma16(short8v a, short8v b, float4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a), __builtin_bit_cast(half8v, b),
-                                                c, 0, 0, 0);
+  if constexpr (std::is_same_v<T, __bf16>)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, a), __builtin_bit_cast(half8v, b),
+                                                  c, 0, 0, 0);
 }
+
+// Pairs of T for the vector-ALU dot products: v_dot2_f32_f16 / _bf16.
+template <typename T>
+struct Pair2 {
+  typedef half2v type;
+  static __device__ __forceinline__ float dot(type a, type b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
+};
+template <>
+struct Pair2<__bf16> {
+  typedef bf16x2v type;
+  static __device__ __forceinline__ float dot(type a, type b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
 
 // 8 int8 weights -> 8 exact fp16 (see the GEMM's dequant8 for the method).
 __device__ __forceinline__ short8v dequant8v(uint32_t d0, uint32_t d1) {
@@ -64,7 +88,7 @@ __device__ __forceinline__ short8v dequant8v(uint32_t d0, uint32_t d1) {
   return out;
 }
 
-template <int TPB, int KS, bool I8, int UNR>
+template <typename T, int TPB, int KS, bool I8, int UNR>
 __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
   // k covered by one lane-load step: fp16 -> 32 (one MFMA), int8 -> 64 (two)
   constexpr int KSTEP = I8 ? 64 : 32;
@@ -129,10 +153,10 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
         if constexpr (I8) {
           const short8v w0 = dequant8v((uint32_t)wv[u][t][0], (uint32_t)wv[u][t][1]);
           const short8v w1 = dequant8v((uint32_t)wv[u][t][2], (uint32_t)wv[u][t][3]);
-          acc[t] = mfma16(w0, __builtin_bit_cast(short8v, xv[u][0]), acc[t]);
-          acc[t] = mfma16(w1, __builtin_bit_cast(short8v, xv[u][1]), acc[t]);
+          acc[t] = mfma16<T>(w0, __builtin_bit_cast(short8v, xv[u][0]), acc[t]);
+          acc[t] = mfma16<T>(w1, __builtin_bit_cast(short8v, xv[u][1]), acc[t]);
         } else {
-          acc[t] = mfma16(__builtin_bit_cast(short8v, wv[u][t]), __builtin_bit_cast(short8v, xv[u][0]), acc[t]);
+          acc[t] = mfma16<T>(__builtin_bit_cast(short8v, wv[u][t]), __builtin_bit_cast(short8v, xv[u][0]), acc[t]);
         }
       }
     }
@@ -181,13 +205,13 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
       float v[4] = {sum[0], sum[1], sum[2], sum[3]};
       if (I8) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] *= (float)((const _Float16*)a.scale)[n + q];
+        for (int q = 0; q < 4; ++q) v[q] *= (float)((const T*)a.scale)[n + q];
       }
       if (a.bias) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] += (float)((const _Float16*)a.bias)[n + q];
+        for (int q = 0; q < 4; ++q) v[q] += (float)((const T*)a.bias)[n + q];
       }
-      _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+      T h[4] = {(T)v[0], (T)v[1], (T)v[2], (T)v[3]};
       *(short4v*)(a.y + ((int64_t)m * a.ldy + n) * 2) = __builtin_bit_cast(short4v, h);
     }
   }
@@ -208,7 +232,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
 // stays a few percent of the MFMA units at HBM speed.
 // (launched for fp16 weights; int8 weights run gemv_pair_i8 below, which
 // keeps this layout and overlaps the first tile's loads with x's staging)
-template <bool I8, int NWIN, int U, int YKEEP>
+template <typename T, bool I8, int NWIN, int U, int YKEEP>
 __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
   constexpr int FPW = I8 ? 4 : 2;     // x fragments per window
@@ -247,9 +271,9 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   __shared__ uint32_t ykeep[4][YKEEP > 0 ? YKEEP : 1][64];
   const int m = lane & 15;
   auto store_pair = [&](int n, uint32_t bits) {
-    _Float16 h2[2];
+    T h2[2];
     __builtin_memcpy(h2, &bits, 4);
-    _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+    T* yrow = (T*)(a.y + ((int64_t)m * a.ldy + n) * 2);
     if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
       *(uint32_t*)yrow = bits;
     } else {
@@ -270,8 +294,8 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       if (n + q < a.N) {
-        if (I8) sc[q] = (float)((const _Float16*)a.scale)[n + q];
-        if (a.bias) bi[q] = (float)((const _Float16*)a.bias)[n + q];
+        if (I8) sc[q] = (float)((const T*)a.scale)[n + q];
+        if (a.bias) bi[q] = (float)((const T*)a.bias)[n + q];
       }
     }
     float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -292,14 +316,14 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
           if constexpr (I8) {
             const short8v lo = dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
             const short8v hi = dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
-            acc0 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
-            acc0 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
-            acc1 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
-            acc1 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
+            acc0 = mfma16<T>(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
+            acc0 = mfma16<T>(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
+            acc1 = mfma16<T>(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
+            acc1 = mfma16<T>(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
           } else {
             const short8v wf = __builtin_bit_cast(short8v, wv[u]);
-            acc0 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
-            acc1 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
+            acc0 = mfma16<T>(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
+            acc1 = mfma16<T>(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
           }
         }
       }
@@ -310,7 +334,7 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
       float v[2] = {acc0[0] + acc1[1], acc0[2] + acc1[3]};
 #pragma unroll
       for (int q = 0; q < 2; ++q) v[q] = v[q] * sc[q] + bi[q];
-      _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+      T h2[2] = {(T)v[0], (T)v[1]};
       const uint32_t bits = __builtin_bit_cast(uint32_t, h2);
       if (YKEEP > 0 && it < YKEEP) ykeep[w][it][lane] = bits;
       else if (m < a.M) store_pair(n, bits);
@@ -335,6 +359,7 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
 // measured slower there (lm_head M = 1 40.3 -> 42.1 us).
 template <int NWIN>
 __global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
+  using T = _Float16;
   constexpr bool I8 = true;
   constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
   constexpr int FPW = I8 ? 4 : 2;     // x fragments per window
@@ -402,14 +427,14 @@ __global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
         if constexpr (I8) {
           const short8v lo = dequant8v((uint32_t)wv[j][0], (uint32_t)wv[j][1]);
           const short8v hi = dequant8v((uint32_t)wv[j][2], (uint32_t)wv[j][3]);
-          acc0 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
-          acc0 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
-          acc1 = mfma16(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
-          acc1 = mfma16(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
+          acc0 = mfma16<T>(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
+          acc0 = mfma16<T>(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
+          acc1 = mfma16<T>(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
+          acc1 = mfma16<T>(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
         } else {
           const short8v wf = __builtin_bit_cast(short8v, wv[j]);
-          acc0 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
-          acc1 = mfma16(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
+          acc0 = mfma16<T>(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
+          acc1 = mfma16<T>(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
         }
       }
     }
@@ -421,13 +446,13 @@ __global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
       const half2v s2 = __builtin_bit_cast(half2v, scb), b2 = __builtin_bit_cast(half2v, bib);
       const float sc0 = I8 ? (float)s2[0] : 1.f, sc1 = I8 ? (float)s2[1] : 1.f;
       const float v[2] = {(acc0[0] + acc1[1]) * sc0 + (float)b2[0], (acc0[2] + acc1[3]) * sc1 + (float)b2[1]};
-      _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+      T* yrow = (T*)(a.y + ((int64_t)m * a.ldy + n) * 2);
       if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
-        _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+        T h2[2] = {(T)v[0], (T)v[1]};
         *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
       } else {
-        if (n < a.N) yrow[0] = (_Float16)v[0];
-        if (n + 1 < a.N) yrow[1] = (_Float16)v[1];
+        if (n < a.N) yrow[0] = (T)v[0];
+        if (n + 1 < a.N) yrow[1] = (T)v[1];
       }
     }
   }
@@ -439,7 +464,7 @@ __global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
 // reduced through LDS.  Each wave loads its own x fragments (x is a few KB
 // and stays in L2), so a tile costs one memory round trip plus the
 // reduction, with no cross-workgroup fix-up.
-template <bool I8, int KS, int U>
+template <typename T, bool I8, int KS, int U>
 __global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
   constexpr int KW = I8 ? 128 : 64;
   constexpr int FPW = I8 ? 4 : 2;
@@ -470,8 +495,8 @@ __global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       if (n + q < a.N) {
-        if (I8) sc[q] = (float)((const _Float16*)a.scale)[n + q];
-        if (a.bias) bi[q] = (float)((const _Float16*)a.bias)[n + q];
+        if (I8) sc[q] = (float)((const T*)a.scale)[n + q];
+        if (a.bias) bi[q] = (float)((const T*)a.bias)[n + q];
       }
     }
   }
@@ -496,14 +521,14 @@ __global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
         if constexpr (I8) {
           const short8v lo = dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
           const short8v hi = dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
-          acc0 = mfma16(lo, __builtin_bit_cast(short8v, xv[u][0]), acc0);
-          acc0 = mfma16(hi, __builtin_bit_cast(short8v, xv[u][1]), acc0);
-          acc1 = mfma16(lo, __builtin_bit_cast(short8v, xv[u][2]), acc1);
-          acc1 = mfma16(hi, __builtin_bit_cast(short8v, xv[u][3]), acc1);
+          acc0 = mfma16<T>(lo, __builtin_bit_cast(short8v, xv[u][0]), acc0);
+          acc0 = mfma16<T>(hi, __builtin_bit_cast(short8v, xv[u][1]), acc0);
+          acc1 = mfma16<T>(lo, __builtin_bit_cast(short8v, xv[u][2]), acc1);
+          acc1 = mfma16<T>(hi, __builtin_bit_cast(short8v, xv[u][3]), acc1);
         } else {
           const short8v wf = __builtin_bit_cast(short8v, wv[u]);
-          acc0 = mfma16(wf, __builtin_bit_cast(short8v, xv[u][0]), acc0);
-          acc1 = mfma16(wf, __builtin_bit_cast(short8v, xv[u][1]), acc1);
+          acc0 = mfma16<T>(wf, __builtin_bit_cast(short8v, xv[u][0]), acc0);
+          acc1 = mfma16<T>(wf, __builtin_bit_cast(short8v, xv[u][1]), acc1);
         }
       }
     }
@@ -520,28 +545,28 @@ __global__ __launch_bounds__(KS * 64) void gemv_pair_ks(VArgs a) {
     float v[2] = {s[0], s[1]};
 #pragma unroll
     for (int q = 0; q < 2; ++q) v[q] = v[q] * sc[q] + bi[q];
-    _Float16* yrow = (_Float16*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+    T* yrow = (T*)(a.y + ((int64_t)m * a.ldy + n) * 2);
     if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
-      _Float16 h2[2] = {(_Float16)v[0], (_Float16)v[1]};
+      T h2[2] = {(T)v[0], (T)v[1]};
       *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
     } else {
-      if (n < a.N) yrow[0] = (_Float16)v[0];
-      if (n + 1 < a.N) yrow[1] = (_Float16)v[1];
+      if (n < a.N) yrow[0] = (T)v[0];
+      if (n + 1 < a.N) yrow[1] = (T)v[1];
     }
   }
 }
 
-template <bool I8>
+template <typename T, bool I8>
 hipError_t launch_pair_ks(const VArgs& v, int ks, hipStream_t stream) {
   const int blocks = (v.N + 7) / 8;
   if (ks >= 16)
-    hipLaunchKernelGGL((gemv_pair_ks<I8, 16, I8 ? 4 : 8>), dim3(blocks), dim3(1024), 0, stream, v);
+    hipLaunchKernelGGL((gemv_pair_ks<T, I8, 16, I8 ? 4 : 8>), dim3(blocks), dim3(1024), 0, stream, v);
   else
-    hipLaunchKernelGGL((gemv_pair_ks<I8, 8, I8 ? 4 : 8>), dim3(blocks), dim3(512), 0, stream, v);
+    hipLaunchKernelGGL((gemv_pair_ks<T, I8, 8, I8 ? 4 : 8>), dim3(blocks), dim3(512), 0, stream, v);
   return hipGetLastError();
 }
 
-template <bool I8>
+template <typename T, bool I8>
 hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   const int tiles = (v.N + 7) / 8;
   int blocks = (tiles + 3) / 4;
@@ -556,9 +581,9 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   if constexpr (I8)
     hipLaunchKernelGGL((gemv_pair_i8<8>), dim3(blocks), dim3(256), 0, stream, v);
   else if (v.M > 4)
-    hipLaunchKernelGGL((gemv_pair<false, 16, 16, 6>), dim3(blocks), dim3(256), 0, stream, v);
+    hipLaunchKernelGGL((gemv_pair<T, false, 16, 16, 6>), dim3(blocks), dim3(256), 0, stream, v);
   else
-    hipLaunchKernelGGL((gemv_pair<false, 16, 16, 0>), dim3(blocks), dim3(256), 0, stream, v);
+    hipLaunchKernelGGL((gemv_pair<T, false, 16, 16, 0>), dim3(blocks), dim3(256), 0, stream, v);
   return hipGetLastError();
 }
 
@@ -569,7 +594,7 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
 // K-steps) is staged in LDS once per workgroup; the 8 partial dot products of
 // a row are summed with lane shuffles at the end.  Workgroups stride over the
 // row groups so each stages x once.
-template <int MM, bool I8, int U>
+template <typename T, int MM, bool I8, int U>
 __global__ __launch_bounds__(256) void gemv_valu(VArgs a, int kpad) {
   constexpr int WPB = 4;
   constexpr int KC = I8 ? 16 : 8;  // k per lane load
@@ -611,7 +636,7 @@ __global__ __launch_bounds__(256) void gemv_valu(VArgs a, int kpad) {
       for (int u = 0; u < U; ++u) {
         if (s0 + u < nsteps) {
           const int k = (s0 + u) * KSTEP + c * KC;
-          half2v wh[KC / 2];
+          typename Pair2<T>::type wh[KC / 2];
           if constexpr (I8) {
             const short8v lo = dequant8v((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
             const short8v hi = dequant8v((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
@@ -623,12 +648,12 @@ __global__ __launch_bounds__(256) void gemv_valu(VArgs a, int kpad) {
 #pragma unroll
           for (int m = 0; m < MM; ++m) {
             if (m < M) {
-              half2v xh[KC / 2];
+              typename Pair2<T>::type xh[KC / 2];
               const char* xp = xs + ((int64_t)m * kpad + k) * 2;
               __builtin_memcpy(&xh[0], xp, 16);
               if constexpr (I8) __builtin_memcpy(&xh[4], xp + 16, 16);
 #pragma unroll
-              for (int q = 0; q < KC / 2; ++q) acc[m] = __builtin_amdgcn_fdot2(wh[q], xh[q], acc[m], false);
+              for (int q = 0; q < KC / 2; ++q) acc[m] = Pair2<T>::dot(wh[q], xh[q], acc[m]);
             }
           }
         }
@@ -648,15 +673,15 @@ __global__ __launch_bounds__(256) void gemv_valu(VArgs a, int kpad) {
       for (int m = m0; m < MM && m < m0 + 8; ++m)
         if (c == m - m0) v = acc[m];
       if (rok && m0 + c < M) {
-        if (I8) v *= (float)((const _Float16*)a.scale)[row];
-        if (a.bias) v += (float)((const _Float16*)a.bias)[row];
-        ((_Float16*)a.y)[(int64_t)(m0 + c) * a.ldy + row] = (_Float16)v;
+        if (I8) v *= (float)((const T*)a.scale)[row];
+        if (a.bias) v += (float)((const T*)a.bias)[row];
+        ((T*)a.y)[(int64_t)(m0 + c) * a.ldy + row] = (T)v;
       }
     }
   }
 }
 
-template <int MM, bool I8>
+template <typename T, int MM, bool I8>
 hipError_t launch_valu(const VArgs& v, hipStream_t stream) {
   constexpr int KSTEP = I8 ? 128 : 64;
   const int kpad = (v.K + KSTEP - 1) / KSTEP * KSTEP;
@@ -665,20 +690,20 @@ hipError_t launch_valu(const VArgs& v, hipStream_t stream) {
   const int cap = 256 * 8;  // enough workgroups to fill every CU several times over
   if (blocks > cap) blocks = cap;
   const size_t lds = (size_t)v.M * kpad * 2;
-  hipLaunchKernelGGL((gemv_valu<MM, I8, 8>), dim3(blocks), dim3(256), lds, stream, v, kpad);
+  hipLaunchKernelGGL((gemv_valu<T, MM, I8, 8>), dim3(blocks), dim3(256), lds, stream, v, kpad);
   return hipGetLastError();
 }
 
-template <bool I8>
+template <typename T, bool I8>
 hipError_t launch_valu_sel(const VArgs& v, hipStream_t stream) {
-  if (v.M == 1) return launch_valu<1, I8>(v, stream);
-  if (v.M == 2) return launch_valu<2, I8>(v, stream);
-  if (v.M <= 4) return launch_valu<4, I8>(v, stream);
-  if (v.M <= 8) return launch_valu<8, I8>(v, stream);
-  return launch_valu<16, I8>(v, stream);
+  if (v.M == 1) return launch_valu<T, 1, I8>(v, stream);
+  if (v.M == 2) return launch_valu<T, 2, I8>(v, stream);
+  if (v.M <= 4) return launch_valu<T, 4, I8>(v, stream);
+  if (v.M <= 8) return launch_valu<T, 8, I8>(v, stream);
+  return launch_valu<T, 16, I8>(v, stream);
 }
 
-template <int TPB, int KS, bool I8>
+template <typename T, int TPB, int KS, bool I8>
 hipError_t launch_cfg(const VArgs& v, hipStream_t stream) {
   // loads in flight per wave: a wave whose K range is long (few tiles, large
   // K) issues 16 steps at a time; short ranges keep 4 (2 for 4-tile groups)
@@ -689,36 +714,36 @@ hipError_t launch_cfg(const VArgs& v, hipStream_t stream) {
   if (const int64_t e = knob(KNOB_GEMV_UNR); e != KNOB_UNSET) unr = e >= 16 ? 16 : (e >= 8 ? 8 : (TPB >= 4 ? 2 : 4));
   if constexpr (TPB < 4) {
     if (unr == 16 && TPB == 1) {
-      hipLaunchKernelGGL((gemv_mfma<1, KS, I8, 16>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+      hipLaunchKernelGGL((gemv_mfma<T, 1, KS, I8, 16>), dim3(blocks), dim3(KS * 64), 0, stream, v);
       return hipGetLastError();
     }
     // (16 waves per workgroup leave 128 VGPRs: 8 steps of two tiles would spill)
     if constexpr (TPB == 1 || KS <= 8) {
       if (unr == 8) {
-        hipLaunchKernelGGL((gemv_mfma<TPB, KS, I8, 8>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+        hipLaunchKernelGGL((gemv_mfma<T, TPB, KS, I8, 8>), dim3(blocks), dim3(KS * 64), 0, stream, v);
         return hipGetLastError();
       }
     }
   }
-  hipLaunchKernelGGL((gemv_mfma<TPB, KS, I8, (TPB >= 4 ? 2 : 4)>), dim3(blocks), dim3(KS * 64), 0, stream, v);
+  hipLaunchKernelGGL((gemv_mfma<T, TPB, KS, I8, (TPB >= 4 ? 2 : 4)>), dim3(blocks), dim3(KS * 64), 0, stream, v);
   return hipGetLastError();
 }
 
-template <bool I8>
+template <typename T, bool I8>
 hipError_t launch_sel(int tpb, int ks, const VArgs& v, hipStream_t stream) {
   if (tpb == 4) {
-    if (ks == 4) return launch_cfg<4, 4, I8>(v, stream);
-    if (ks == 8) return launch_cfg<4, 8, I8>(v, stream);
-    return launch_cfg<4, 16, I8>(v, stream);
+    if (ks == 4) return launch_cfg<T, 4, 4, I8>(v, stream);
+    if (ks == 8) return launch_cfg<T, 4, 8, I8>(v, stream);
+    return launch_cfg<T, 4, 16, I8>(v, stream);
   }
   if (tpb == 2) {
-    if (ks == 4) return launch_cfg<2, 4, I8>(v, stream);
-    if (ks == 8) return launch_cfg<2, 8, I8>(v, stream);
-    return launch_cfg<2, 16, I8>(v, stream);
+    if (ks == 4) return launch_cfg<T, 2, 4, I8>(v, stream);
+    if (ks == 8) return launch_cfg<T, 2, 8, I8>(v, stream);
+    return launch_cfg<T, 2, 16, I8>(v, stream);
   }
-  if (ks == 4) return launch_cfg<1, 4, I8>(v, stream);
-  if (ks == 8) return launch_cfg<1, 8, I8>(v, stream);
-  return launch_cfg<1, 16, I8>(v, stream);
+  if (ks == 4) return launch_cfg<T, 1, 4, I8>(v, stream);
+  if (ks == 8) return launch_cfg<T, 1, 8, I8>(v, stream);
+  return launch_cfg<T, 1, 16, I8>(v, stream);
 }
 
 }  // namespace
@@ -831,15 +856,25 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.kg = 1;
   v.ws = nullptr;
   const GemvPlan g = gemv_plan(p);
-  if (g.valu) return p.w_int8 ? launch_valu_sel<true>(v, stream) : launch_valu_sel<false>(v, stream);
-  if (g.pair) return p.w_int8 ? launch_pair<true>(v, stream) : launch_pair<false>(v, stream);
-  if (g.pair_ks) return p.w_int8 ? launch_pair_ks<true>(v, g.ks, stream) : launch_pair_ks<false>(v, g.ks, stream);
+  const bool bf = p.dtype == DT_BF16;  // bf16 x, W, bias, y (fp16 weights otherwise; int8 takes fp16 x)
+  if (g.valu)
+    return p.w_int8 ? launch_valu_sel<_Float16, true>(v, stream)
+                    : (bf ? launch_valu_sel<__bf16, false>(v, stream) : launch_valu_sel<_Float16, false>(v, stream));
+  if (g.pair)
+    return p.w_int8 ? launch_pair<_Float16, true>(v, stream)
+                    : (bf ? launch_pair<__bf16, false>(v, stream) : launch_pair<_Float16, false>(v, stream));
+  if (g.pair_ks)
+    return p.w_int8 ? launch_pair_ks<_Float16, true>(v, g.ks, stream)
+                    : (bf ? launch_pair_ks<__bf16, false>(v, g.ks, stream)
+                          : launch_pair_ks<_Float16, false>(v, g.ks, stream));
   const int64_t need = g.kg > 1 ? gemv_workspace_bytes(p) : 0;
   if (need > 0 && p.ws && p.ws_bytes >= need && ((uintptr_t)p.ws % 256) == 0) {
     v.kg = g.kg;
     v.ws = (char*)p.ws;
   }
-  return p.w_int8 ? launch_sel<true>(g.tpb, g.ks, v, stream) : launch_sel<false>(g.tpb, g.ks, v, stream);
+  return p.w_int8 ? launch_sel<_Float16, true>(g.tpb, g.ks, v, stream)
+                  : (bf ? launch_sel<__bf16, false>(g.tpb, g.ks, v, stream)
+                        : launch_sel<_Float16, false>(g.tpb, g.ks, v, stream));
 }
 
 }  // namespace hxmi

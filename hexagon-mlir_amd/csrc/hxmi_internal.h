@@ -82,7 +82,7 @@ struct GemmProblem {
 
 // Wg[n][k] = fp16(W[n][k] * g[k]): folds an RMSNorm weight into the linear
 // layer that consumes the normalised activations.
-hipError_t launch_fold_rms_weight(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+hipError_t launch_fold_rms_weight(int dtype, const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
                                   int64_t ldwg, hipStream_t stream);
 
 // s[n] = fp16 scale covering max_k |W[n][k]| / 127, q[n][k] = rint(W[n][k] / s[n]):
@@ -121,14 +121,15 @@ bool gemm_fast_path_ok(const GemmProblem& p);
 int gemm_pick_tile(const GemmProblem& p);
 
 struct GemvProblem {
-  const void* x;      // [M,K] fp16
-  const void* W;      // [N,K] fp16 or int8
+  const void* x;      // [M,K] fp16 (bf16 with dtype DT_BF16)
+  const void* W;      // [N,K] fp16 / bf16, or int8
   const void* scale;  // [N] fp16 (int8 weights only)
-  const void* bias;   // [N] fp16 or null
-  void* y;            // [M,N] fp16
+  const void* bias;   // [N] x's type, or null
+  void* y;            // [M,N] x's type
   int64_t M, N, K;
   int64_t ldx, ldw, ldy;
   int w_int8;
+  int dtype = DT_F16;  // DT_F16 or DT_BF16 (int8 weights: fp16 activations)
   void* ws;  // optional workspace for K split over workgroups
   int64_t ws_bytes;
 };

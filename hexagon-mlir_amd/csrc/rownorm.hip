@@ -218,22 +218,27 @@ hipError_t launch_softmax(const RowProblem& p, hipStream_t stream) {
 
 namespace {
 
-__global__ __launch_bounds__(256) void fold_rms_weight(const _Float16* W, const _Float16* g, _Float16* Wg, int64_t N,
-                                                       int64_t K, int64_t ldw, int64_t ldwg) {
+template <typename T>
+__global__ __launch_bounds__(256) void fold_rms_weight(const T* W, const T* g, T* Wg, int64_t N, int64_t K,
+                                                       int64_t ldw, int64_t ldwg) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= N * K) return;
   const int64_t n = i / K, k = i - n * K;
-  Wg[n * ldwg + k] = (_Float16)((float)W[n * ldw + k] * (float)g[k]);
+  Wg[n * ldwg + k] = (T)((float)W[n * ldw + k] * (float)g[k]);
 }
 
 }  // namespace
 
-hipError_t launch_fold_rms_weight(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
-                                  int64_t ldwg, hipStream_t stream) {
+hipError_t launch_fold_rms_weight(int dtype, const void* W, const void* g, void* Wg, int64_t N, int64_t K,
+                                  int64_t ldw, int64_t ldwg, hipStream_t stream) {
   const int64_t blocks = (N * K + 255) / 256;
   if (blocks >= (1ll << 31)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(fold_rms_weight, dim3((unsigned)blocks), dim3(256), 0, stream, (const _Float16*)W,
-                     (const _Float16*)g, (_Float16*)Wg, N, K, ldw, ldwg);
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL(fold_rms_weight<__bf16>, dim3((unsigned)blocks), dim3(256), 0, stream, (const __bf16*)W,
+                       (const __bf16*)g, (__bf16*)Wg, N, K, ldw, ldwg);
+  else
+    hipLaunchKernelGGL(fold_rms_weight<_Float16>, dim3((unsigned)blocks), dim3(256), 0, stream, (const _Float16*)W,
+                       (const _Float16*)g, (_Float16*)Wg, N, K, ldw, ldwg);
   return hipGetLastError();
 }
 

@@ -42,6 +42,7 @@ SIGNATURES = {
     "hxmi_bgemm_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_bgemm_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _F, _P], _I),
     "hxmi_gemv_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
+    "hxmi_gemv_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "hxmi_gemv_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "hxmi_gemv_w8a16": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
     "hxmi_w8a16_workspace_bytes": ([_I64, _I64, _I64], _I64),
@@ -52,7 +53,9 @@ SIGNATURES = {
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
     "hxmi_attention_ex_f16": ([_P, _P, _P, _P] + [_I64] * 13 + [_P, _I64, _I64, _I64, _I, _F, _P], _I),
     "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
+    "hxmi_rmsnorm_linear_bf16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_fold_rmsnorm_weight_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_quantize_int8_rows_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_lwp_record": ([_P, _I64, ctypes.c_uint32, _P], _I),
     "hxmi_lwp_clock_hz": ([], _I64),
@@ -313,19 +316,20 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None
 
 
 def fold_rms_weight(w: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
-    """w [N,K] with the RMSNorm weight g [K] folded in: fp16(w[n,k] * g[k]), the
+    """w [N,K] with the RMSNorm weight g [K] folded in: T(w[n,k] * g[k]) (T = fp16 or bf16), the
     weight rms_norm_linear takes (fold a packed gate/up weight after packing)."""
     _require_gpu(w, g)
-    if w.dtype != torch.float16 or g.dtype != torch.float16:
-        raise HxmiError("fold_rms_weight takes fp16 tensors")
+    if w.dtype not in (torch.float16, torch.bfloat16) or g.dtype != w.dtype:
+        raise HxmiError("fold_rms_weight takes fp16 or bf16 tensors of one dtype")
     if w.dim() != 2:
         raise HxmiError("fold_rms_weight takes a 2-D weight")
     N, K = w.shape
     ldw = _rowmajor(w, "w")
-    g = _vec(g, K, torch.float16, "g")
-    out = torch.empty((N, K), dtype=torch.float16, device=w.device)
-    _check(load_library().hxmi_fold_rmsnorm_weight_f16(w.data_ptr(), g.data_ptr(), out.data_ptr(), N, K, ldw, K,
-                                                       _stream(w)))
+    g = _vec(g, K, w.dtype, "g")
+    out = torch.empty((N, K), dtype=w.dtype, device=w.device)
+    lib = load_library()
+    fn = lib.hxmi_fold_rmsnorm_weight_f16 if w.dtype == torch.float16 else lib.hxmi_fold_rmsnorm_weight_bf16
+    _check(fn(w.data_ptr(), g.data_ptr(), out.data_ptr(), N, K, ldw, K, _stream(w)))
     return out
 
 
@@ -360,8 +364,8 @@ def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, 
         raise HxmiError("rscale_out and rscale_in are exclusive")
     if rscale_out is not None and not rscale_out.is_contiguous():
         raise HxmiError("rscale_out must be contiguous")
-    if x.dtype != torch.float16 or w_folded.dtype != torch.float16:
-        raise HxmiError("rms_norm_linear takes fp16 tensors")
+    if x.dtype not in (torch.float16, torch.bfloat16) or w_folded.dtype != x.dtype:
+        raise HxmiError("rms_norm_linear takes fp16 or bf16 tensors of one dtype")
     if epilogue not in (None, "silu_mul"):
         raise HxmiError(f"rms_norm_linear epilogue must be None or 'silu_mul', got {epilogue!r}")
     if bias is not None and epilogue is not None:
@@ -378,34 +382,36 @@ def rms_norm_linear(x: torch.Tensor, w_folded: torch.Tensor, eps: float = 1e-5, 
     out2 = out.reshape(M, nout)
     rs_out = _vec(rscale_out, M, torch.float32, "rscale_out")
     rs_in = _vec(rscale_in, M, torch.float32, "rscale_in")
-    bias = _vec(bias, N, torch.float16, "bias")
+    bias = _vec(bias, N, x.dtype, "bias")
     epi = EPILOGUES["bias"] if bias is not None else EPILOGUES[epilogue]
-    _check(load_library().hxmi_rmsnorm_linear_f16(x2.data_ptr(), w_folded.data_ptr(), out2.data_ptr(), _ptr(bias),
-                                                  M, N, K, _rowmajor(x2, "x"), _rowmajor(w_folded, "w"),
-                                                  _rowmajor(out2, "out"), epi, float(eps), _ptr(rs_out), _ptr(rs_in),
-                                                  _stream(x)))
+    lib = load_library()
+    fn = lib.hxmi_rmsnorm_linear_f16 if x.dtype == torch.float16 else lib.hxmi_rmsnorm_linear_bf16
+    _check(fn(x2.data_ptr(), w_folded.data_ptr(), out2.data_ptr(), _ptr(bias),
+              M, N, K, _rowmajor(x2, "x"), _rowmajor(w_folded, "w"), _rowmajor(out2, "out"), epi, float(eps),
+              _ptr(rs_out), _ptr(rs_in), _stream(x)))
     return out2.reshape(*lead, nout)
 
 
 def gemv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
          out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Decode linear y[M,N] = x[M,K] @ w[N,K].T (+ bias); HBM-streaming for M <= 16."""
+    """Decode linear y[M,N] = x[M,K] @ w[N,K].T (+ bias); HBM-streaming for M <= 16.  fp16 or bf16."""
     _require_gpu(x, w, bias, out)
-    if x.dtype != torch.float16 or w.dtype != torch.float16:
-        raise HxmiError("gemv takes fp16 x and w")
+    if x.dtype not in (torch.float16, torch.bfloat16) or w.dtype != x.dtype:
+        raise HxmiError("gemv takes fp16 or bf16 x and w of one dtype")
     ldx, ldw = _rowmajor(x, "x"), _rowmajor(w, "w")
     M, K = x.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise HxmiError(f"x {tuple(x.shape)} and w {tuple(w.shape)} disagree on K")
-    bias = _vec(bias, N, torch.float16, "bias")
+    bias = _vec(bias, N, x.dtype, "bias")
     if out is None:
-        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
     ldy = _rowmajor(out, "out")
     lib = load_library()
     ws = _workspace(lib.hxmi_gemv_workspace_bytes(M, N, K), x.device)
-    _check(lib.hxmi_gemv_f16(x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, ldx, ldw, ldy,
-                             _ptr(ws), 0 if ws is None else ws.numel() * 4, _stream(x)))
+    fn = lib.hxmi_gemv_f16 if x.dtype == torch.float16 else lib.hxmi_gemv_bf16
+    _check(fn(x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), M, N, K, ldx, ldw, ldy,
+              _ptr(ws), 0 if ws is None else ws.numel() * 4, _stream(x)))
     return out
 
 

@@ -168,6 +168,11 @@ int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int
 int hxmi_gemv_f16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
                   int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Same contract as hxmi_gemv_f16 with bf16 x, W, bias and y (fp32
+ * accumulation; the same kernels and launch plans on bf16 MFMA / dot). */
+int hxmi_gemv_bf16(const void* x, const void* W, const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                   int64_t ldx, int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes a contiguous hxmi_gemv_f16 call of this shape can use (0: never split). */
 int64_t hxmi_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
@@ -239,10 +244,21 @@ int hxmi_rmsnorm_linear_f16(const void* x, const void* Wg, void* C, const void* 
                             int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps, float* rscale_out,
                             const float* rscale_in, void* stream);
 
+/* Same contract as hxmi_rmsnorm_linear_f16 with bf16 x, Wg, bias and C
+ * (statistics and accumulation in fp32). */
+int hxmi_rmsnorm_linear_bf16(const void* x, const void* Wg, void* C, const void* bias, int64_t M, int64_t N,
+                             int64_t K, int64_t ldx, int64_t ldw, int64_t ldc, int epilogue, float eps,
+                             float* rscale_out, const float* rscale_in, void* stream);
+
 /* Wg[n,k] = fp16(W[n,k] * g[k]) (fp32 product, one rounding): the weight
  * hxmi_rmsnorm_linear_f16 takes.  W, Wg [N,K] (leading dims ldw, ldwg), g [K]. */
 int hxmi_fold_rmsnorm_weight_f16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
                                  int64_t ldwg, void* stream);
+
+/* The bf16 form of hxmi_fold_rmsnorm_weight_f16 (bf16 W, g, Wg), for
+ * hxmi_rmsnorm_linear_bf16. */
+int hxmi_fold_rmsnorm_weight_bf16(const void* W, const void* g, void* Wg, int64_t N, int64_t K, int64_t ldw,
+                                  int64_t ldwg, void* stream);
 
 /*
  * Per-output-channel symmetric int8 quantisation, the weight layout

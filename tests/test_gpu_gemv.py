@@ -416,3 +416,45 @@ def test_w8a16_pair_ragged_rows_strided_out(pkg, dev, gemv_path, M):
     torch.cuda.synchronize()
     assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
     assert torch.all(big[:, N:].cpu() == 7.0)  # nothing written past N
+
+
+# ---- bf16 -------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("K,N", QWEN)
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_bf16_qwen_shapes(pkg, dev, M, K, N):
+    """bf16 activations and weights on the same kernels and plans as fp16
+    (bf16 MFMA / v_dot2_f32_bf16), fp32 accumulation, bf16 out."""
+    x = normal((M, K), 300 + M, dtype=torch.bfloat16)
+    w = normal((N, K), 400 + K % 7, 0.02, dtype=torch.bfloat16)
+    y = pkg.gemv(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(np32(x), np32(w))) <= TOL
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu", "pair", "ksplit"])
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_gemv_bf16_every_kernel(pkg, dev, knobs, path, M):
+    """Each of the four GEMV kernels forced in turn, with a bias, on a shape
+    every one of them takes (K <= 1024 for the whole-line kernel, ragged N)."""
+    knobs(gemv_path=path)
+    K, N = 1024 if path != "ksplit" else 2048, 1020
+    x = normal((M, K), 11, dtype=torch.bfloat16)
+    w = normal((N, K), 12, 0.03, dtype=torch.bfloat16)
+    b = normal((N,), 13, dtype=torch.bfloat16)
+    y = pkg.gemv(x.to(dev), w.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(np32(x), np32(w), np32(b))) <= TOL
+
+
+def test_gemv_bf16_exact_integers(pkg, dev):
+    """Small integers are exact in bf16 and their sums exact in fp32: every
+    output bf16-rounds the exact product."""
+    g = torch.Generator().manual_seed(14)
+    x = torch.randint(-3, 4, (4, 896), generator=g).to(torch.bfloat16)
+    w = torch.randint(-3, 4, (2048, 896), generator=g).to(torch.bfloat16)
+    y = pkg.gemv(x.to(dev), w.to(dev)).cpu()
+    exact = (x.double() @ w.double().T).to(torch.bfloat16)
+    assert torch.equal(y, exact)

@@ -201,3 +201,39 @@ def test_rms_norm_linear_bias_every_tile(pkg, dev, force_tile, tile):
     for y, wf, w, b in ((q, wqf, wq, bq), (k, wkf, wk, bk)):
         assert ref.max_rel_err(np32(y), ref.linear(xn_exact, np32(wf.cpu()), b.numpy())) <= TOL
         assert ref.max_err_vs_scale(np32(y), ref.linear(xn, w.numpy(), b.numpy())) <= TOL
+
+
+# ---- bf16 -------------------------------------------------------------------------------------------
+
+
+def test_fold_weight_bf16_is_one_rounding(pkg, dev):
+    w = normal((300, 520), 21, 0.02, dtype=torch.bfloat16)
+    g = (1 + 0.02 * torch.randn(520, generator=torch.Generator().manual_seed(22))).to(torch.bfloat16)
+    wf = pkg.fold_rms_weight(w.to(dev), g.to(dev)).cpu()
+    exp = (w.float() * g.float()[None, :]).to(torch.bfloat16)
+    assert torch.equal(wf, exp)
+
+
+def test_rms_norm_linear_bf16_block_pair(pkg, dev):
+    """The TinyLlama QKV call (statistics in the GEMM, row scales published)
+    and gate/up with SiLU-mul reusing them, in bf16."""
+    M, K, N, I = 512, 2048, 2560, 1408
+    bf = torch.bfloat16
+    x = normal((M, K), 23, dtype=bf)
+    g = (1 + 0.02 * torch.randn(K, generator=torch.Generator().manual_seed(24))).to(bf)
+    w = normal((N, K), 25, 0.02, dtype=bf)
+    wg, wu = normal((I, K), 26, 0.02, dtype=bf), normal((I, K), 27, 0.02, dtype=bf)
+    wf = pkg.fold_rms_weight(w.to(dev), g.to(dev))
+    wguf = pkg.fold_rms_weight(pkg.pack_gate_up(wg.to(dev), wu.to(dev)), g.to(dev))
+    rs = torch.empty(M, dtype=torch.float32, device=dev)
+    y = pkg.rms_norm_linear(x.to(dev), wf, 1e-5, rscale_out=rs)
+    h = pkg.rms_norm_linear(x.to(dev), wguf, 1e-5, epilogue="silu_mul", rscale_in=rs)
+    torch.cuda.synchronize()
+    assert y.dtype == bf and h.dtype == bf
+    xf = np32(x)
+    r = 1.0 / np.sqrt((xf * xf).mean(-1) + 1e-5)
+    assert np.allclose(rs.cpu().numpy(), r, rtol=1e-5)
+    xn = ref.rms_norm(xf, np.ones(K, np.float32), 1e-5)
+    assert ref.max_rel_err(np32(y.cpu()), ref.linear(xn, np32(wf.cpu()))) <= TOL
+    wfu = ref.unpack_gate_up_cols(np32(wguf.cpu()).T, wguf.shape[0])
+    assert ref.max_rel_err(np32(h.cpu()), ref.silu_mul_linear(xn, wfu[0].T, wfu[1].T)) <= TOL
