@@ -418,9 +418,11 @@ def cpu_baseline(runs: int = 7) -> dict:
 
 
 def profile_suite(pkg, torch, dev, timer) -> None:
-    """Launches for counter runs: 4096^3 NT GEMM and the Qwen2.5-0.5B lm_head
-    GEMVs, each warmed up by time, then 5 launches (weights rotate over
-    copies so none is cache-resident), then five 256 MiB copies."""
+    """Launches for counter runs, each warmed up by time, then 5 launches:
+    4096^3 NT GEMM, the Qwen2.5-0.5B lm_head fp16 / int8 GEMVs (M = 1, 16)
+    and the int8 GEMM at M = 256 (weights rotate over copies so none is
+    cache-resident), the ViT-B/16 batch-8 fused attention, fc1 and fc2,
+    softmax [18912, 197], RMSNorm [512, 2048]; then five 256 MiB copies."""
     g = torch.Generator().manual_seed(1)
     a = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(dev)
     b = (torch.rand(4096, 4096, generator=g) * 2 - 1).half().to(dev)
@@ -447,12 +449,47 @@ def profile_suite(pkg, torch, dev, timer) -> None:
         timer._warm(w8)
         for i in range(5):
             w8(i)
+    # int8 lm_head at M = 256 (the MFMA GEMM with int8 B), three weight copies
+    x = torch.randn(256, H, generator=g).half().to(dev)
+    y = torch.empty(256, V, dtype=torch.float16, device=dev)
+    w8g = lambda i=0: pkg.w8a16_linear(x, qs[i % 3], sc, out=y)
+    timer._warm(w8g)
+    for i in range(5):
+        w8g(i)
+    del ws, qs
+    # ViT-B/16 batch 8: fused attention, fc1 (+bias, tanh-GELU), fc2 (+bias)
+    B, S, Hh, D, E, F = VIT_B, VIT_S, VIT_H, VIT_D, VIT_E, VIT_F
+    q, k, v = (torch.randn(B, Hh, S, D, generator=g).half().to(dev) for _ in range(3))
+    o = torch.empty_like(q)
+    xv = torch.randn(B * S, E, generator=g).half().to(dev)
+    w1 = (torch.randn(F, E, generator=g) * 0.02).half().to(dev)
+    b1 = (torch.randn(F, generator=g) * 0.02).half().to(dev)
+    w2 = (torch.randn(E, F, generator=g) * 0.02).half().to(dev)
+    b2 = (torch.randn(E, generator=g) * 0.02).half().to(dev)
+    h1 = torch.empty(B * S, F, dtype=torch.float16, device=dev)
+    h2 = torch.empty(B * S, E, dtype=torch.float16, device=dev)
+    att = lambda i=0: pkg.attention(q, k, v, D ** -0.5, out=o)
+    fc1 = lambda i=0: pkg.linear(xv, w1, b1, epilogue="gelu_tanh", out=h1)
+    fc2 = lambda i=0: pkg.linear(h1, w2, b2, out=h2)
+    # row kernels: softmax [18912, 197] (scale 0.125), RMSNorm [512, 2048]
+    sm_x = torch.randn(B * Hh * S, S, generator=g).half().to(dev)
+    sm_y = torch.empty_like(sm_x)
+    rn_x = torch.randn(512, 2048, generator=g).half().to(dev)
+    rn_w = torch.ones(2048, dtype=torch.float16, device=dev)
+    rn_y = torch.empty_like(rn_x)
+    smx = lambda i=0: pkg.softmax(sm_x, 0.125, out=sm_y)
+    rms = lambda i=0: pkg.rms_norm(rn_x, rn_w, 1e-5, out=rn_y)
+    for fn in (att, fc1, fc2, smx, rms):
+        timer._warm(fn)
+        for _ in range(5):
+            fn()
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log("[bench] profile suite: 4096^3 GEMM, lm_head GEMV fp16 M=1/16, int8 M=1/16, 5 x 256 MiB copies")
+    log("[bench] profile suite: 4096^3 GEMM, lm_head GEMV fp16 M=1/16, int8 M=1/16/256, ViT-B/16 attention / fc1 / "
+        "fc2, softmax [18912, 197], RMSNorm [512, 2048], 5 x 256 MiB copies")
 
 
 def traffic_from_profiles():
