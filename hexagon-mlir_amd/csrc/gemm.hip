@@ -140,6 +140,10 @@ int gemm_pick_tile(const GemmProblem& p) {
     // it, and the latency-bound small shapes want the most workgroups
     // (measured on the Qwen2.5-0.5B int8 shapes at M = 256)
     float eff = c.eff;
+    // the three-stage 8-wave 256x128 tile pays once K is long enough to keep
+    // its deeper prefetch busy (TinyLlama gate/up, K = 2048: 33.1 -> 30.7 us
+    // against 128x128 at two per CU; ViT fc1, K = 768: 19.4 -> 20.6 us)
+    if (!i8 && c.id == TILE_256x128_W8 && p.K >= 1536) eff = 0.95f;
     if (i8 && (c.id == TILE_128x128_W8 || c.id == TILE_256x128_W8)) eff = 0.80f;
     if (i8 && c.id == TILE_64x64) eff = 0.60f;
     const int64_t tm = (p.M + c.bm - 1) / c.bm, tn = (p.N + c.bn - 1) / c.bn;

@@ -774,10 +774,15 @@ struct TileShape {
 // flight while two or three workgroups still fit per CU.  Measured on the
 // TinyLlama block in sequence (weights not resident in L2): 91.0 -> 79.3 us;
 // four stages, at half the workgroups per CU, gave 87.1 us.
+// The 384-row tiles (256x128 and 128x256, 48 KB per stage) hold one
+// workgroup per CU with two stages already, so a third costs no occupancy:
+// TinyLlama gate/up with SiLU-mul on the 8-wave 256x128 tile went 33.7 ->
+// 30.7 us (the 8-wave 128x128 tile at two per CU: 33.1 us; with three or
+// four stages, one per CU, 40.8 / 42.0 us).
 constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 256, 128, 128, 64, 2},  // TILE_256x256
-    {128, 256, 64, 128, 64, 2},   // TILE_128x256
-    {256, 128, 128, 64, 64, 2},   // TILE_256x128
+    {128, 256, 64, 128, 64, 3},   // TILE_128x256
+    {256, 128, 128, 64, 64, 3},   // TILE_256x128
     {128, 128, 64, 64, 64, 2},    // TILE_128x128
     {64, 128, 32, 64, 64, 3},     // TILE_64x128 (3 stages: see below)
     {128, 64, 64, 32, 64, 3},     // TILE_128x64
@@ -787,7 +792,7 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {128, 128, 64, 64, 32, 4},    // TILE_128x128_K32S4
     {256, 128, 128, 64, 32, 4},   // TILE_256x128_K32S4
     {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
-    {256, 128, 64, 64, 64, 2},         // TILE_256x128_W8
+    {256, 128, 64, 64, 64, 3},         // TILE_256x128_W8
     {128, 128, 32, 64, 64, 2},         // TILE_128x128_W8
 };
 

@@ -110,7 +110,7 @@ enum TileId {
   TILE_128x128_K32S4,
   TILE_256x128_K32S4,
   TILE_256x256_PP,  // 8 waves, ping-pong schedule, 32-deep K-steps, 3 stages
-  TILE_256x128_W8,  // 8 waves of 64x64
+  TILE_256x128_W8,  // 8 waves of 64x64, 3 stages
   TILE_128x128_W8,  // 8 waves of 32x64
   TILE_COUNT
 };
