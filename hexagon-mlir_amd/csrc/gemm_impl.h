@@ -272,7 +272,7 @@ __device__ __forceinline__ void pp_barrier() {
 // loads its next step's fragments from LDS and issues the global->LDS loads,
 // so every SIMD's MFMA pipe alternates between its two waves.
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool NN, typename T, int EPI, bool OUTF32,
-          bool BI8 = false, bool PP = false, bool RMS = false, bool RAGGED = false>
+          bool BI8 = false, bool PP = false, bool RMS = false, bool RAGGED = false, int SB = 0>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -281,14 +281,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   constexpr int RPIK = 1024 / RB;       // k-contiguous rows per 1 KB wave instruction
   constexpr int A_BYTES = BM * RB;
   constexpr int B_BYTES = BI8 ? BN * BK : BN * RB;  // int8 B stays int8 in LDS
-  constexpr int STAGE = A_BYTES + B_BYTES;
+  // STAGES LDS stages of A, SBS of B (SB = 0: as many as A).  More B stages
+  // than A ones prefetch B further ahead, for B streamed from HBM while A
+  // stays in L2.  LDS holds the A stages, then the B stages.
+  constexpr int SBS = SB ? SB : STAGES;
+  constexpr int A_REGION = STAGES * A_BYTES;
   constexpr int BNO = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int SROW = BNO * 2 + 16;
   constexpr int EPI_BYTES = OUTF32 ? 0 : BM * SROW;
-  constexpr int SMEM = (STAGES * STAGE > EPI_BYTES) ? STAGES * STAGE : EPI_BYTES;
+  constexpr int SMEM = (A_REGION + SBS * B_BYTES > EPI_BYTES) ? A_REGION + SBS * B_BYTES : EPI_BYTES;
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(STAGES >= 2 && STAGES <= 4, "STAGES");
-  static_assert(SMEM <= 160 * 1024, "LDS budget");
+  static_assert(SBS >= STAGES && SBS <= 8 && (!PP || SBS == STAGES), "B stages");
+  static_assert(SMEM <= 159 * 1024, "LDS budget (with the split-K flag)");
   static_assert(BM % (RPIK * NW) == 0, "A tile rows per wave");
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
   static_assert(!BI8 || (!NN && BK == 64 && BN % (16 * NW) == 0), "int8 B: [N,K], BK 64, 16-row loads");
@@ -296,6 +301,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(!RMS || (!NN && !BI8 && !PP && !OUTF32), "RMSNorm prologue: NT, standard schedule");
   static_assert(!RAGGED || (!BI8 && !PP && !RMS), "ragged K: plain fp16 / bf16 operands, standard schedule");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+  auto sa = [&](int i) { return smem + i * A_BYTES; };              // A stage i
+  auto sb = [&](int i) { return smem + A_REGION + i * B_BYTES; };   // B stage i
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -358,18 +365,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   }
   const int nk = (K + BK - 1) / BK;
 
-  // Loads of K-step kt into LDS stage `stage`; a step past the end issues
+  // Loads of K-step kt into A / B stage `stage`; a step past the end issues
   // loads against an empty buffer (all zeros, nothing touched).
-  auto issue = [&](int kt, int stage) {
+  auto issueA = [&](int kt, int stage) {
     const int k0 = kt * BK;
     const bool live = kt < nk;
-    char* sA_ = smem + stage * STAGE;
-    char* sB_ = sA_ + A_BYTES;
+    char* sA_ = sa(stage);
     const __amdgpu_buffer_rsrc_t rA = make_rsrc(Ab + (int64_t)k0 * 2, live ? bytesA - 2u * k0 : 0u);
     const uint32_t vA = (k0 + cA * 8) < K ? voffA : kOOB;
 #pragma unroll
     for (int i = 0; i < IA; ++i)
       load_lds16(rA, (HXMI_LDS void*)to_lds(sA_ + (i * NW + w) * 1024), vA + i * stepA);
+  };
+  auto issueB = [&](int kt, int stage) {
+    const int k0 = kt * BK;
+    const bool live = kt < nk;
+    char* sB_ = sb(stage);
     if constexpr (NN) {
       const uint32_t rows = (uint32_t)min(BK, K - k0);
       const __amdgpu_buffer_rsrc_t rB = make_rsrc(Bb + (int64_t)k0 * a.ldb * 2, live ? rows * bytesB : 0u);
@@ -389,6 +400,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       for (int i = 0; i < IB; ++i)
         load_lds16(rB, (HXMI_LDS void*)to_lds(sB_ + (i * NW + w) * 1024), vB + i * stepB);
     }
+  };
+  auto issue = [&](int kt, int stage) {
+    issueA(kt, stage);
+    issueB(kt, stage);
   };
 
   // Byte offset of this lane's 16-byte chunk in a k-contiguous fragment of
@@ -478,8 +493,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     int st = 0, stw = D;
     for (int kt = 0; kt < nk; ++kt) {
       issue(kt + D, stw);
-      const char* sA_ = smem + st * STAGE;
-      const char* sB_ = sA_ + A_BYTES;
+      const char* sA_ = sa(st);
+      const char* sB_ = sb(st);
       static_for<SUBS>([&](auto S) { read_frags(fa[decltype(S)::value], fb[decltype(S)::value], sA_, sB_, decltype(S)::value, kt); });
       wait_vmcnt<(D - 1) * NVM>();
       pp_barrier();
@@ -496,29 +511,40 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     }
     if (grp == 0) pp_barrier();
   } else {
+  // Issue order, step by step: step t issues A(t + STAGES), then
+  // B(t + SBS); the prologue runs the virtual steps t = -SBS .. -1 (A only
+  // where t + STAGES >= 0).  Step kt needs A(kt) and B(kt); with SBS >
+  // STAGES, B(kt) was issued before A(kt), so waiting for A(kt) leaves in
+  // flight the B issued just after it plus every later step's loads.
+  constexpr int WB = SBS > STAGES ? IB : 0;
 #pragma unroll
-  for (int p = 0; p < STAGES; ++p) issue(p, p);
-  wait_vmcnt<(STAGES - 1) * NVM>();
+  for (int t = -SBS; t < 0; ++t) {
+    if (t + STAGES >= 0) issueA(t + STAGES, t + STAGES);
+    issueB(t + SBS, t + SBS);
+  }
+  wait_vmcnt<(STAGES - 1) * NVM + WB>();
   __syncthreads();
   short8v fa[2][TM], fb[2][TN];
-  read_frags(fa[0], fb[0], smem, smem + A_BYTES, 0, 0);
-  int st = 0;
+  read_frags(fa[0], fb[0], sa(0), sb(0), 0, 0);
+  int st = 0, stb = 0;
   for (int kt = 0; kt < nk; ++kt) {
     const int st1 = (st + 1 == STAGES) ? 0 : st + 1;
-    const char* sA_ = smem + st * STAGE;
-    const char* sB_ = sA_ + A_BYTES;
+    const int stb1 = (stb + 1 == SBS) ? 0 : stb + 1;
+    const char* sA_ = sa(st);
+    const char* sB_ = sb(stb);
     static_for<SUBS>([&](auto S) {
       constexpr int s = decltype(S)::value;
       constexpr int nxt = (s + 1) & 1;
       if constexpr (s + 1 < SUBS) {
         read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1, kt);
       } else {
-        wait_vmcnt<(STAGES - 2) * NVM>();
+        wait_vmcnt<(STAGES - 2) * NVM + WB>();
         __syncthreads();
         // fragment reads first, then the refill loads: the same order as the
         // schedule below, so the loads can be spread between the MFMAs
-        read_frags(fa[nxt], fb[nxt], smem + st1 * STAGE, smem + st1 * STAGE + A_BYTES, 0, kt + 1);
-        issue(kt + STAGES, st);
+        read_frags(fa[nxt], fb[nxt], sa(st1), sb(stb1), 0, kt + 1);
+        issueA(kt + STAGES, st);
+        issueB(kt + SBS, stb);
       }
 #pragma unroll
       for (int i = 0; i < TN; ++i)
@@ -532,6 +558,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       __builtin_amdgcn_sched_barrier(0);
     });
     st = st1;
+    stb = stb1;
   }
   }
   wait_vmcnt0();
@@ -766,6 +793,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 struct TileShape {
   int BM, BN, WM, WN, BK, STAGES;
   bool PP = false;
+  int SB = 0;  // B stages (0: as many as A)
 };
 
 // The small tiles run three LDS stages: their K-steps are short (a 64x64x64
@@ -801,12 +829,13 @@ hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr TileShape s = kTiles[TILE];
   constexpr int threads = (s.BM / s.WM) * (s.BN / s.WN) * 64;
   const int64_t blocks = (int64_t)k.tiles_m * k.tiles_n * k.batch;
-  // int8 B: BK 64, and three LDS stages where they fit (the weights stream
-  // from HBM, so the deeper prefetch pays)
-  constexpr int W8_STAGE = s.BM * 128 + s.BN * 64;
-  constexpr int W8_STAGES = 3 * W8_STAGE <= 160 * 1024 ? 3 : 2;
-  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? W8_STAGES : s.STAGES), NN, T, EPI, OUTF32, BI8,
-                                (s.PP && !BI8 && !RMS), RMS, RAGGED>),
+  // int8 B: BK 64, two A stages (A is L2-resident) and up to six B stages
+  // in the LDS that three stages of both took (same workgroups per CU): the
+  // weights stream from HBM, so B is prefetched several K-steps ahead
+  constexpr int W8_A = s.BM * 128, W8_B = s.BN * 64;
+  constexpr int W8_SB = W8_A / W8_B + 3 > 6 ? 6 : W8_A / W8_B + 3;
+  hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8,
+                                (s.PP && !BI8 && !RMS), RMS, RAGGED, (BI8 ? W8_SB : s.SB)>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
 }
