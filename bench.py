@@ -313,6 +313,55 @@ def bench_decode_step(pkg, torch, dev, timer, iters):
             "bytes": nbytes, "launches": L * len(shapes) + 1}
 
 
+def bench_decode_full(pkg, torch, dev, timer, iters):
+    """The whole one-token Qwen2.5-0.5B forward at position 0 (what the
+    reference's Qwen run computes: RMSNorms, q|k|v with bias, attention over
+    the one key, o + residual, gate|up, SiLU-mul, down + residual, final norm,
+    lm_head), 0.99 GB of fp16 weights: as the persistent decode kernel (one
+    launch + the lm_head GEMV) and as the same step from separate library
+    launches (RMSNorm, GEMV, torch elementwise glue), both in HIP graphs.  The
+    two outputs are compared before anything is timed."""
+    H, KV, I, V, L, heads, kvh = 896, 128, 4864, 151936, 24, 14, 2
+    g = torch.Generator(device=dev).manual_seed(11)
+    rnd = lambda *s, std=0.02, mean=0.0: (torch.randn(*s, generator=g, device=dev) * std + mean).half()
+    st = pkg.hxmi.DecoderStack(
+        w_qkv=rnd(L, H + 2 * KV, H), b_qkv=rnd(L, H + 2 * KV, std=0.1), w_o=rnd(L, H, H), w_gu=rnd(L, 2 * I, H),
+        w_down=rnd(L, H, I), g_attn=rnd(L, H, std=0.1, mean=1.0), g_mlp=rnd(L, H, std=0.1, mean=1.0),
+        g_final=rnd(H, std=0.1, mean=1.0), heads=heads, kv_heads=kvh, eps=1e-6, w_lm=rnd(V, H))
+    x = torch.randn(H, generator=g, device=dev).half()
+    grp, hd = heads // kvh, H // heads
+
+    def chained(_i=0):
+        xs = x.view(1, H)
+        for l in range(L):
+            h = pkg.rms_norm(xs, st.g_attn[l], st.eps)
+            qkv = pkg.gemv(h, st.w_qkv[l], st.b_qkv[l])
+            att = qkv[:, H + KV:].view(kvh, hd).repeat_interleave(grp, dim=0).reshape(1, H)
+            xs = xs + pkg.gemv(att, st.w_o[l])
+            h = pkg.rms_norm(xs, st.g_mlp[l], st.eps)
+            gu = pkg.gemv(h, st.w_gu[l])
+            a = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+            xs = xs + pkg.gemv(a, st.w_down[l])
+        return pkg.gemv(pkg.rms_norm(xs, st.g_final, st.eps), st.w_lm)
+
+    out = pkg.hxmi.decode_step(x, st)
+    ref_logits = chained()
+    torch.cuda.synchronize()
+    status = pkg.hxmi.decode_status()
+    err = ((out["logits"].float() - ref_logits[0].float()).abs().max() / ref_logits.float().abs().max()).item()
+    if status != 0 or not err < 1e-2:
+        raise SystemExit(f"[bench] decode step check failed: status {status}, logits rel err {err}")
+    nbytes = 2 * sum(t.numel() for t in (st.w_qkv, st.b_qkv, st.w_o, st.w_gu, st.w_down, st.g_attn, st.g_mlp,
+                                         st.g_final, st.w_lm))
+    res = {"bytes": nbytes, "logits_rel_err_vs_chained": round(err, 5)}
+    for name, fn in (("persistent", lambda i: pkg.hxmi.decode_step(x, st)), ("chained_launches", chained)):
+        ms = timer.graph_ms(fn, iters)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    del st
+    return res
+
+
 def bench_rows(pkg, torch, dev, timer, iters):
     out = {}
     g = torch.Generator().manual_seed(4)
@@ -520,6 +569,9 @@ def main() -> int:
                     help="for rocprofv3 counter runs: the 4096^3 fp16 NT GEMM and the lm_head decode GEMVs (fp16 "
                          "M=1 and M=16, int8 M=1), each warmed up and then launched 5 times, then the 256 MiB copy "
                          "calibration, and exit")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="for rocprofv3: the full Qwen2.5-0.5B one-token forward, as the persistent decode kernel "
+                         "and as separate launches, checked against each other and timed, and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: hexagon-mlir_amd has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -537,6 +589,9 @@ def main() -> int:
 
     if args.profile_suite:
         profile_suite(pkg, torch, dev, timer)
+        return 0
+    if args.profile_decode:
+        log(f"[bench] full decode forward {bench_decode_full(pkg, torch, dev, timer, 5)}")
         return 0
     step, gate_up, block_tensors, block_buf = make_block(pkg, torch, dev)
     fl = tinyllama_flops()
@@ -617,6 +672,8 @@ def main() -> int:
         log(f"[bench] w8a16 lm_head M1 {w8['M1_896x151936']}")
         secondary["decode_step_qwen_m1"] = bench_decode_step(pkg, torch, dev, timer, 10)
         log(f"[bench] decode step {secondary['decode_step_qwen_m1']}")
+        secondary["decode_forward_qwen_m1"] = bench_decode_full(pkg, torch, dev, timer, 5)
+        log(f"[bench] full decode forward {secondary['decode_forward_qwen_m1']}")
         secondary.update(bench_rows(pkg, torch, dev, timer, 100))
         secondary["vit_b16_block_b8"] = bench_vit(pkg, torch, dev, timer, 20)
         log(f"[bench] rows/vit done")

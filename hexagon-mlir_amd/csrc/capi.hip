@@ -491,6 +491,83 @@ int hxmi_quantize_int8_rows_f16(const void* W, int8_t* q, void* s, int64_t N, in
   return from_hip(hxmi::launch_quantize_int8_rows(W, q, s, N, K, ldw, ldq, (hipStream_t)stream), name);
 }
 
+int64_t hxmi_decode_workspace_bytes(int64_t hidden, int64_t kv_dim, int64_t intermediate) {
+  if (hidden <= 0 || kv_dim <= 0 || intermediate <= 0) return 0;
+  return hxmi::decode_workspace_bytes(hidden, kv_dim, intermediate);
+}
+
+int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_o, const void* w_gu,
+                         const void* w_down, const void* g_attn, const void* g_mlp, const void* g_final,
+                         const void* w_lm, void* qkv_out, void* x_out, void* h_out, void* logits, int64_t layers,
+                         int64_t hidden, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t intermediate,
+                         int64_t vocab, float eps, int64_t timeout_us, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+  const char* name = "hxmi_decode_step_f16";
+  REQUIRE(layers > 0 && hidden > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && intermediate > 0,
+          "%s: sizes must be positive", name);
+  REQUIRE(layers <= 4096, "%s: at most 4096 layers, got %lld", name, (long long)layers);
+  REQUIRE(x && w_qkv && w_o && w_gu && w_down && g_attn && g_mlp && g_final && h_out && workspace,
+          "%s: null pointer", name);
+  REQUIRE(!w_lm || (logits && vocab > 0), "%s: w_lm needs logits and vocab > 0", name);
+  REQUIRE(eps >= 0.f, "%s: eps must be >= 0", name);
+  const int64_t kv_dim = kv_heads * head_dim;
+  REQUIRE(workspace_bytes >= hxmi::decode_workspace_bytes(hidden, kv_dim, intermediate),
+          "%s: workspace of %lld bytes, needs hxmi_decode_workspace_bytes() = %lld", name,
+          (long long)workspace_bytes, (long long)hxmi::decode_workspace_bytes(hidden, kv_dim, intermediate));
+  REQUIRE(al(workspace, 256), "%s: workspace must be 256-byte aligned", name);
+  if (!hxmi::decode_shape_ok(hidden, heads, kv_heads, head_dim, intermediate))
+    return fail(HXMI_ERR_UNSUPPORTED,
+                "%s: unsupported shape (hidden %lld, heads %lld, kv_heads %lld, head_dim %lld, intermediate %lld)",
+                name, (long long)hidden, (long long)heads, (long long)kv_heads, (long long)head_dim,
+                (long long)intermediate);
+  for (const void* p : {x, w_qkv, w_o, w_gu, w_down, g_attn, g_mlp, g_final, (const void*)h_out})
+    REQUIRE(al(p, 16), "%s: x, weights and outputs must be 16-byte aligned", name);
+  REQUIRE(!x_out || al(x_out, 16), "%s: x_out must be 16-byte aligned", name);
+  REQUIRE(!qkv_out || al(qkv_out, 2), "%s: qkv_out must be 2-byte aligned", name);
+  hxmi::DecodeProblem p{};
+  p.x = x;
+  p.w_qkv = w_qkv;
+  p.b_qkv = b_qkv;
+  p.w_o = w_o;
+  p.w_gu = w_gu;
+  p.w_down = w_down;
+  p.g_attn = g_attn;
+  p.g_mlp = g_mlp;
+  p.g_final = g_final;
+  p.qkv_out = qkv_out;
+  p.x_out = x_out;
+  p.h_out = h_out;
+  p.ws = (uint32_t*)workspace;
+  p.L = layers;
+  p.H = hidden;
+  p.heads = heads;
+  p.kv_heads = kv_heads;
+  p.head_dim = head_dim;
+  p.I = intermediate;
+  p.eps = eps;
+  p.timeout_us = timeout_us;
+  const hipError_t e = hxmi::launch_decode_step(p, (hipStream_t)stream);
+  if (e != hipSuccess) return from_hip(e, name);
+  if (!w_lm) return ok();
+  return gemv_common(hxmi::DT_F16, name, h_out, w_lm, nullptr, logits, 1, vocab, hidden, hidden, hidden, vocab,
+                     nullptr, 0, stream);
+}
+
+int hxmi_decode_status(void* workspace, int clear, int* status, void* stream) {
+  REQUIRE(workspace && status, "hxmi_decode_status: null pointer");
+  uint32_t word = 0;
+  const uint32_t* err = (const uint32_t*)workspace + hxmi::DECODE_WS_ERROR_WORD;
+  hipError_t e = hipMemcpyAsync(&word, err, sizeof(word), hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  if (e == hipSuccess && clear && word) {
+    static const uint32_t zero = 0;
+    e = hipMemcpyAsync((uint32_t*)err, &zero, sizeof(zero), hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  }
+  *status = (int)word;
+  return from_hip(e, "hxmi_decode_status");
+}
+
 int hxmi_lwp_record(uint32_t* records, int64_t slot, uint32_t id, void* stream) {
   const char* name = "hxmi_lwp_record";
   REQUIRE(records, "%s: null record buffer", name);

@@ -172,6 +172,34 @@ struct AttnProblem {
 
 hipError_t launch_attention(const AttnProblem& p, hipStream_t stream);
 
+// One-token decoder step of a Llama / Qwen2 stack (persistent kernel).
+struct DecodeProblem {
+  const void* x;        // [H] fp16: the token's embedding row
+  const void* w_qkv;    // [L, H + 2*kv_dim, H]: q rows, k rows, v rows
+  const void* b_qkv;    // [L, H + 2*kv_dim] or null
+  const void* w_o;      // [L, H, H]
+  const void* w_gu;     // [L, 2*I, H]: gate rows, then up rows
+  const void* w_down;   // [L, H, I]
+  const void* g_attn;   // [L, H] RMSNorm weights before attention
+  const void* g_mlp;    // [L, H] RMSNorm weights before the MLP
+  const void* g_final;  // [H]
+  void* qkv_out;        // [L, H + 2*kv_dim] or null
+  void* x_out;          // [H] final hidden state before the last norm, or null
+  void* h_out;          // [H] normalised final hidden state
+  uint32_t* ws;         // decode_workspace_bytes(), zero-filled before first use
+  int64_t L, H, heads, kv_heads, head_dim, I;
+  float eps;
+  int64_t timeout_us;  // bound of every wait inside the kernel
+};
+
+int64_t decode_workspace_bytes(int64_t H, int64_t kv_dim, int64_t I);
+// Word of the decode workspace that records an expired wait (sticky).
+constexpr int DECODE_WS_ERROR_WORD = 3;
+// hipErrorNotSupported: shape outside the kernel's limits (the caller falls
+// back to per-GEMV launches).
+hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream);
+bool decode_shape_ok(int64_t H, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t I);
+
 // Region profiling: record `slot` of `records` (3 words each) = {id, wall
 // clock low word, high word}, taken when the marker runs on `stream`.
 hipError_t launch_lwp_mark(uint32_t* records, int64_t slot, uint32_t id, hipStream_t stream);

@@ -8,6 +8,7 @@ raises.
 from __future__ import annotations
 
 import collections
+import dataclasses
 import contextlib
 import ctypes
 import pathlib
@@ -57,6 +58,9 @@ SIGNATURES = {
     "hxmi_fold_rmsnorm_weight_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_fold_rmsnorm_weight_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_quantize_int8_rows_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
+    "hxmi_decode_step_f16": ([_P] * 14 + [_I64] * 7 + [_F, _I64, _P, _I64, _P], _I),
+    "hxmi_decode_workspace_bytes": ([_I64, _I64, _I64], _I64),
+    "hxmi_decode_status": ([_P, _I, ctypes.POINTER(_I), _P], _I),
     "hxmi_lwp_record": ([_P, _I64, ctypes.c_uint32, _P], _I),
     "hxmi_lwp_clock_hz": ([], _I64),
     "hexkl_matmul_f16f16_f32": ([_I64, _I64, _I64, _P, _P, _P], _I),
@@ -584,6 +588,120 @@ def hexkl_matmul(act: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     _check(load_library().hexkl_matmul_f16f16_f32(n_row, n_col, n_inner, out.data_ptr(), act.data_ptr(),
                                                   w.data_ptr()))
     return out
+
+
+@dataclasses.dataclass
+class DecoderStack:
+    """fp16 weights of a Llama / Qwen2 decoder stack, stacked per layer, on one
+    GPU (H hidden, I intermediate, kv_dim = kv_heads * head_dim, head_dim =
+    H / heads):
+
+    w_qkv [L, H + 2*kv_dim, H] (q rows, k rows, v rows), b_qkv [L, H + 2*kv_dim]
+    or None, w_o [L, H, H], w_gu [L, 2*I, H] (gate rows, then up rows), w_down
+    [L, H, I], g_attn and g_mlp [L, H] (RMSNorm weights), g_final [H], w_lm
+    [vocab, H] or None (no logits)."""
+    w_qkv: torch.Tensor
+    b_qkv: Optional[torch.Tensor]
+    w_o: torch.Tensor
+    w_gu: torch.Tensor
+    w_down: torch.Tensor
+    g_attn: torch.Tensor
+    g_mlp: torch.Tensor
+    g_final: torch.Tensor
+    heads: int
+    kv_heads: int
+    eps: float
+    w_lm: Optional[torch.Tensor] = None
+
+    @property
+    def dims(self) -> tuple[int, int, int, int]:
+        """(layers, hidden, intermediate, kv_dim)"""
+        L, nqkv, H = self.w_qkv.shape
+        return L, H, self.w_gu.shape[1] // 2, (nqkv - H) // 2
+
+
+_DECODE_WS: "dict[tuple, torch.Tensor]" = {}
+
+
+def _decode_key(device: torch.device, shape: tuple) -> tuple:
+    return (device.index if device.index is not None else torch.cuda.current_device(),
+            torch.cuda.current_stream(device).cuda_stream, shape)
+
+
+def _decode_workspace(device: torch.device, shape: tuple, nbytes: int) -> torch.Tensor:
+    """The decode workspace of the current stream of `device` for one stack
+    shape (hidden, kv_dim, intermediate): it carries the step's published
+    vectors and running tag from call to call, so it is kept (zero-filled
+    when created) and shared neither between streams nor between shapes."""
+    key = _decode_key(device, shape)
+    ws = _DECODE_WS.get(key)
+    if ws is None:
+        ws = torch.zeros((nbytes + 255) // 256 * 64, dtype=torch.int32, device=device)
+        _DECODE_WS[key] = ws
+    return ws
+
+
+def decode_step(x: torch.Tensor, stack: DecoderStack, *, out_qkv: bool = False,
+                timeout_us: int = 0) -> dict:
+    """One-token forward of the decoder stack at position 0 (empty KV cache)
+    from the token's embedding row x [H] (fp16), as one persistent kernel
+    (plus the lm_head GEMV when stack.w_lm is set).  Returns {"h": final
+    normalised hidden state [H], "x": hidden state before the final norm [H],
+    "logits": [vocab] or None, "qkv": [L, H + 2*kv_dim] or None}.  A wait
+    inside the kernel longer than timeout_us (0: one second) ends the launch
+    early; decode_status() reports it."""
+    L, H, inter, kv_dim = stack.dims
+    ts = [x, stack.w_qkv, stack.b_qkv, stack.w_o, stack.w_gu, stack.w_down, stack.g_attn, stack.g_mlp,
+          stack.g_final, stack.w_lm]
+    _require_gpu(*ts)
+    for t in ts:
+        if t is not None and (t.dtype != torch.float16 or not t.is_contiguous()):
+            raise HxmiError("decode_step takes contiguous fp16 tensors")
+    head_dim = H // stack.heads
+    want = {"w_o": (L, H, H), "w_gu": (L, 2 * inter, H), "w_down": (L, H, inter), "g_attn": (L, H),
+            "g_mlp": (L, H), "g_final": (H,)}
+    for name, shape in want.items():
+        if tuple(getattr(stack, name).shape) != shape:
+            raise HxmiError(f"{name} is {tuple(getattr(stack, name).shape)}, expected {shape}")
+    if stack.b_qkv is not None and tuple(stack.b_qkv.shape) != (L, H + 2 * kv_dim):
+        raise HxmiError("b_qkv must be [L, H + 2*kv_dim]")
+    if x.numel() != H:
+        raise HxmiError(f"x has {x.numel()} elements, expected {H}")
+    if stack.kv_heads * head_dim != kv_dim or stack.heads * head_dim != H:
+        raise HxmiError("w_qkv rows do not match heads / kv_heads")
+    dev = x.device
+    h = torch.empty(H, dtype=torch.float16, device=dev)
+    xo = torch.empty(H, dtype=torch.float16, device=dev)
+    qkv = torch.empty((L, H + 2 * kv_dim), dtype=torch.float16, device=dev) if out_qkv else None
+    vocab = 0 if stack.w_lm is None else stack.w_lm.shape[0]
+    if stack.w_lm is not None and tuple(stack.w_lm.shape) != (vocab, H):
+        raise HxmiError("w_lm must be [vocab, H]")
+    logits = torch.empty(vocab, dtype=torch.float16, device=dev) if vocab else None
+    lib = load_library()
+    nbytes = lib.hxmi_decode_workspace_bytes(H, kv_dim, inter)
+    ws = _decode_workspace(dev, (H, kv_dim, inter), nbytes)
+    _check(lib.hxmi_decode_step_f16(
+        x.data_ptr(), stack.w_qkv.data_ptr(), _ptr(stack.b_qkv), stack.w_o.data_ptr(), stack.w_gu.data_ptr(),
+        stack.w_down.data_ptr(), stack.g_attn.data_ptr(), stack.g_mlp.data_ptr(), stack.g_final.data_ptr(),
+        _ptr(stack.w_lm), _ptr(qkv), xo.data_ptr(), h.data_ptr(), _ptr(logits), L, H, stack.heads, stack.kv_heads,
+        head_dim, inter, vocab, float(stack.eps), int(timeout_us), ws.data_ptr(), ws.numel() * 4, _stream(x)))
+    return {"h": h, "x": xo, "logits": logits, "qkv": qkv}
+
+
+def decode_status(device: Optional[torch.device] = None, clear: bool = True) -> int:
+    """Error words of the current stream's decode workspaces after their work
+    has finished: 0 = every decode_step so far completed its waits, 1 = a
+    wait expired (that launch's outputs are undefined).  clear resets them."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    stream = torch.cuda.current_stream(device).cuda_stream
+    dev_index = device.index if device.index is not None else torch.cuda.current_device()
+    status = 0
+    for (d, s, _), ws in _DECODE_WS.items():
+        if d == dev_index and s == stream:
+            st = ctypes.c_int(0)
+            _check(load_library().hxmi_decode_status(ws.data_ptr(), int(clear), ctypes.byref(st), stream))
+            status |= st.value
+    return status
 
 
 def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:

@@ -321,6 +321,61 @@ int hxmi_attention_ex_f16(const void* q, const void* k, const void* v, void* o, 
                           float scale, void* stream);
 
 /*
+ * One-token decoder step of a Llama / Qwen2 stack of `layers` layers at
+ * position 0 (empty KV cache), fp16 in and out, fp32 accumulation, as ONE
+ * persistent cooperative launch (plus the lm_head GEMV when w_lm is given):
+ *   x_0 = x; for each layer l:
+ *     h   = rmsnorm(x_l, g_attn[l]);   qkv = h . w_qkv[l]^T (+ b_qkv[l])
+ *     att = attention of the single token: query head i gets v of key/value
+ *           head i / (heads / kv_heads)  (softmax over one key is 1; RoPE at
+ *           position 0 is the identity)
+ *     x1  = x_l + att . w_o[l]^T
+ *     h2  = rmsnorm(x1, g_mlp[l]);     [g | u] = h2 . w_gu[l]^T
+ *     x_{l+1} = x1 + (silu(g) * u) . w_down[l]^T
+ *   h_out = rmsnorm(x_L, g_final);     logits = h_out . w_lm^T
+ * rmsnorm(x, g) = g * fp16(x * rsqrt(mean(x^2) + eps)) with the mean in
+ * fp32; each projection output, the SiLU, the product and each residual sum
+ * is rounded to fp16, as in the HF fp16 forward.
+ * Layouts (device, contiguous; kv_dim = kv_heads * head_dim): x [H] (the
+ * token's embedding row); w_qkv [L, H + 2*kv_dim, H] (q rows, k rows, v
+ * rows); b_qkv [L, H + 2*kv_dim] or NULL; w_o [L, H, H]; w_gu [L, 2*I, H]
+ * (gate rows, then up rows); w_down [L, H, I]; g_attn, g_mlp [L, H];
+ * g_final [H]; w_lm [vocab, H] or NULL.
+ * Outputs: h_out [H]; logits [vocab] when w_lm is given; qkv_out
+ * [L, H + 2*kv_dim] (its k and v rows are what a KV cache appends) or NULL;
+ * x_out [H] = x_L or NULL.
+ * Limits: heads * head_dim == H, H % 8 == 0, H <= 2048, I % 8 == 0,
+ * I <= 6144, head_dim % 8 == 0, kv_dim <= 512; x, the weights and the
+ * outputs 16-byte aligned.  Other shapes: HXMI_ERR_UNSUPPORTED.
+ * workspace: hxmi_decode_workspace_bytes(H, kv_dim, I) bytes of device
+ * memory, zero-filled once after allocation.  It carries the published
+ * phase outputs and a running tag from call to call: one call at a time
+ * per workspace, and one stack shape (H, kv_dim, I) per workspace -- zero
+ * it again before using it for another shape.
+ * timeout_us: bound of every wait inside the kernel (0: one second).  A
+ * wait that expires ends the launch early with the workspace's error word
+ * set (hxmi_decode_status) and the outputs undefined.
+ * Replaces: the reference's Qwen2.5-0.5B forward of a one-token prompt at
+ * position 0 with the cache off (benchmark_models/run_qwen2.5-0.5b.py:
+ * 171-173, 224-233), which it compiles into one generic matmul per
+ * projection (TilingPass.cpp:108-251) and separate elementwise kernels.
+ */
+int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_o, const void* w_gu,
+                         const void* w_down, const void* g_attn, const void* g_mlp, const void* g_final,
+                         const void* w_lm, void* qkv_out, void* x_out, void* h_out, void* logits, int64_t layers,
+                         int64_t hidden, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t intermediate,
+                         int64_t vocab, float eps, int64_t timeout_us, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/* Workspace bytes of hxmi_decode_step_f16 for these sizes. */
+int64_t hxmi_decode_workspace_bytes(int64_t hidden, int64_t kv_dim, int64_t intermediate);
+
+/* Waits for `stream`, then reads the error word of a decode workspace into
+ * *status (0: every launch so far finished its waits; 1: a wait expired)
+ * and, with clear != 0, resets it. */
+int hxmi_decode_status(void* workspace, int clear, int* status, void* stream);
+
+/*
  * Region profiling hook: enqueues on `stream` a one-wave marker that, when it
  * runs (after every kernel enqueued before it on that stream has finished),
  * writes record `slot` of `records` -- three uint32 words {id, t low word,

@@ -35,6 +35,11 @@ Parity status per function (how each is pinned, see tests/test_oracle.py):
                               is_causal, enable_gqa and torch's lower-right
                               causal bias; one-hot and fully-masked closed
                               forms; mask shift invariance
+  decode_step                 transformers' Qwen2ForCausalLM on one token at
+                              position 0 (fp32, and its fp16 forward with
+                              fp16 rounding on); closed forms: zero o/down
+                              projections, kv-head routing of each query head
+                              (tests/test_decode_oracle.py)
   vtcm_tile_sizes             the reference's lit expectation
                               (vtcm_tiling_static.mlir:80-88) and the
                               footprint rule it encodes
@@ -207,6 +212,57 @@ def sdpa(q, k, v, scale=None, mask=None, causal: int = 0, kv_group: int = 1) -> 
         e = np.exp(z)
         p = e / np.sum(e, axis=-1, keepdims=True)
     return np.matmul(p, v32)
+
+
+# ---- one-token decoder step --------------------------------------------------------------
+
+
+def decode_step(x, w_qkv, b_qkv, w_o, w_gu, w_down, g_attn, g_mlp, g_final, heads: int, kv_heads: int,
+                eps: float, w_lm=None, fp16: bool = True) -> dict:
+    """Forward of a Llama / Qwen2 decoder stack on ONE token at position 0
+    with an empty KV cache -- what benchmark_models/run_qwen2.5-0.5b.py
+    :171-173,224-233 runs through the reference (prompt "Hi", use_cache off,
+    position_ids [0]).  Per layer (HF Qwen2DecoderLayer order):
+      h = RMSNorm(x) ; qkv = h W_qkv^T + b ; att[head i] = v[kv head i // (heads/kv_heads)]
+      x = x + att W_o^T ; h = RMSNorm(x) ; [g|u] = h W_gu^T ; x = x + (silu(g)*u) W_down^T
+    then h = RMSNorm(x, g_final), logits = h W_lm^T.  With one key the
+    softmax weight is exactly 1 and RoPE at position 0 is the identity
+    (cos 1, sin 0), so the attention output is v.  w_qkv [L, H + 2*kv, H]
+    (q, k, v rows), w_gu [L, 2I, H] (gate rows, then up rows).
+    fp16=True rounds to fp16 where the HF fp16 forward does (RMSNorm as
+    rms_norm_hf, each projection output, SiLU, the product, each residual
+    sum); fp16=False is the plain fp32 forward."""
+    L, nqkv, H = np.shape(w_qkv)
+    kv = (nqkv - H) // 2
+    hd = H // heads
+    grp = heads // kv_heads
+    r16 = (lambda a: a.astype(np.float16).astype(F32)) if fp16 else (lambda a: a)
+
+    def norm(v, g):
+        if fp16:
+            return rms_norm_hf(v, g, eps).astype(F32)
+        return rms_norm(v, g, eps)
+
+    xs = _f32(x).reshape(H)
+    qkv_all = []
+    for l in range(L):
+        h = norm(xs, g_attn[l])
+        qkv = h @ _f32(w_qkv[l]).T
+        if b_qkv is not None:
+            qkv = qkv + _f32(b_qkv[l])
+        qkv = r16(qkv)
+        qkv_all.append(qkv)
+        v = qkv[H + kv:].reshape(kv_heads, hd)
+        att = v[np.arange(heads) // grp].reshape(H)
+        xs = r16(xs + r16(att @ _f32(w_o[l]).T))
+        h = norm(xs, g_mlp[l])
+        gu = r16(h @ _f32(w_gu[l]).T)
+        inter = gu.shape[0] // 2
+        a = r16(r16(silu(gu[:inter])) * gu[inter:])
+        xs = r16(xs + r16(a @ _f32(w_down[l]).T))
+    h = norm(xs, g_final)
+    logits = None if w_lm is None else r16(h @ _f32(w_lm).T)
+    return {"h": h, "x": xs, "logits": logits, "qkv": np.stack(qkv_all)}
 
 
 # ---- weight-only int8 ----------------------------------------------------------------

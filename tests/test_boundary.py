@@ -194,3 +194,29 @@ def test_noalloc_gemm_rejects_partials_beyond_its_scratch(pkg):
         msg = lib.hxmi_last_error()  # (the next successful call clears it)
     assert rc == 1
     assert b"device scratch" in msg
+
+
+def test_decode_step_rejects_before_launch(pkg):
+    lib = pkg.load_library()
+    need = lib.hxmi_decode_workspace_bytes(896, 128, 4864)
+    assert need == 4 * (64 + 8 * (2 * 896 + 128 + 4864))
+    assert lib.hxmi_decode_workspace_bytes(0, 128, 4864) == 0
+    P = 4096  # 256-byte aligned stand-in addresses: every call below fails before touching them
+
+    def call(layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64, inter=4864, ws_bytes=need, ptr=P, ws=P,
+             w_lm=None, logits=None, vocab=0):
+        return lib.hxmi_decode_step_f16(ptr, P, None, P, P, P, P, P, P, w_lm, None, None, P, logits, layers,
+                                        hidden, heads, kv_heads, head_dim, inter, vocab, 1e-6, 0, ws, ws_bytes,
+                                        None)
+
+    assert call(layers=0) == 1 and "positive" in lib.hxmi_last_error().decode()
+    assert call(ptr=None) == 1 and "null" in lib.hxmi_last_error().decode()
+    assert call(ws_bytes=need - 4) == 1 and "workspace" in lib.hxmi_last_error().decode()
+    assert call(ws=P + 16) == 1 and "256-byte" in lib.hxmi_last_error().decode()
+    assert call(w_lm=P) == 1 and "w_lm" in lib.hxmi_last_error().decode()
+    assert call(ptr=P + 2) == 1 and "16-byte" in lib.hxmi_last_error().decode()
+    # shapes outside the kernel's limits: heads * head_dim != hidden, hidden > 2048, intermediate > 6144
+    assert call(heads=13) == 2
+    assert call(hidden=4096, heads=64, ws_bytes=1 << 20) == 2
+    assert call(inter=8192, ws_bytes=1 << 20) == 2
+    assert "unsupported shape" in lib.hxmi_last_error().decode()
