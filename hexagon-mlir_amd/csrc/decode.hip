@@ -47,6 +47,8 @@
 // workspace's sticky error word and an abort word that every other wait
 // also checks, so all waves leave.  The last wave to leave resets the abort
 // word and advances the tag base.
+#include <algorithm>
+
 #include "hxmi_common.h"
 #include "hxmi_internal.h"
 
@@ -777,6 +779,24 @@ bool decode_shape_ok(int64_t H, int64_t heads, int64_t kv_heads, int64_t head_di
          I <= 4 * kNC * 64 * kPoll && H <= 4 * kNC * 64 * kPoll;
 }
 
+// Whether a grid of G workgroups can stream an L-layer stack.  A phase too
+// large for the ring runs tile by tile and frees a tile's bytes only after
+// the tile is consumed, while a loader batch is issued only once its end is
+// at most one ring past the freed bytes: one 16-row tile (or the whole
+// phase, when a workgroup has fewer rows) must therefore fit the ring less
+// a batch and a chunk.  Row counts are the largest share of a workgroup
+// (ceil(rows / G)).  The stream offset of a layer is an int.
+static bool decode_grid_ok(int64_t H, int64_t kv, int64_t I, int64_t L, int64_t G) {
+  const int64_t room = kRing - (int64_t)(kBatch + 1) * kChunk;
+  auto share = [&](int64_t n) { return (n + G - 1) / G; };
+  auto tile_fits = [&](int64_t rows, int64_t K) { return std::min<int64_t>(rows, 16) * K * 2 <= room; };
+  const int64_t r0 = share(H + 2 * kv), r1 = share(H), r2 = 2 * share(I), r3 = share(H);
+  if (!tile_fits(r0, H) || !tile_fits(r1, H) || !tile_fits(r2, H) || !tile_fits(r3, I)) return false;
+  auto pad = [](int64_t b) { return (b + kChunk - 1) / kChunk * kChunk; };
+  const int64_t layer = pad(r0 * H * 2) + pad(r1 * H * 2) + pad(r2 * H * 2) + pad(r3 * I * 2);
+  return L * layer < ((int64_t)1 << 31) - layer;
+}
+
 int64_t decode_workspace_bytes(int64_t H, int64_t kv_dim, int64_t I) {
   return 4 * ((int64_t)kCtrlWords + kCopies * (2 * (int64_t)rup64(H) + rup64(kv_dim) + rup64(I)));
 }
@@ -794,6 +814,7 @@ hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream) {
       hipSuccess)
     return e;
   if (!coop || per_cu < 1 || cus < 1) return hipErrorNotSupported;
+  if (!decode_grid_ok(p.H, p.kv_heads * p.head_dim, p.I, p.L, cus)) return hipErrorNotSupported;
 
   DArgs a{};
   a.x = (const char*)p.x;
