@@ -69,12 +69,14 @@ __device__ __forceinline__ short4v lds_read_tr16(const char* p) {
   return __builtin_bit_cast(short4v, v);
 }
 
-// Wave reductions without LDS round trips: DPP swaps inside each row of 16
-// lanes (quad permutes, then rotations by 4 and 8 that cover the row), then
-// v_permlane16_swap / v_permlane32_swap across rows.  Every lane receives
-// the result.
-template <typename Op>
+// Reductions over aligned groups of W lanes (16, 32 or the whole wave of 64)
+// without LDS round trips: DPP swaps inside each row of 16 lanes (quad
+// permutes, then rotations by 4 and 8 that cover the row), then
+// v_permlane16_swap (pairs of rows: 32 lanes) and v_permlane32_swap (the
+// two halves).  Every lane of a group receives its group's result.
+template <int W = 64, typename Op>
 __device__ __forceinline__ float wave_reduce_dpp(float v, Op op) {
+  static_assert(W == 16 || W == 32 || W == 64, "group of 16, 32 or 64 lanes");
   auto dpp = [](float x, int ctrl) {
     switch (ctrl) {  // the control word must be a constant
       case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
@@ -87,8 +89,10 @@ __device__ __forceinline__ float wave_reduce_dpp(float v, Op op) {
   v = op(v, dpp(v, 1));  // quad_perm [2,3,0,1]
   v = op(v, dpp(v, 2));  // row_ror:4
   v = op(v, dpp(v, 3));  // row_ror:8
+  if (W == 16) return v;
   const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = op(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  if (W == 32) return v;
   const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return op(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }

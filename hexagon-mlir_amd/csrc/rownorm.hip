@@ -105,42 +105,76 @@ __global__ __launch_bounds__(256) void rmsnorm_any(RArgs a) {
 
 // ---- softmax: y = exp(s*x - max) / sum ---------------------------------------
 
-// EPL elements per lane, strided by 64 (coalesced 2-byte loads; any
-// alignment).  The max and the sum go through DPP and lane-swap reductions
-// (no LDS round trip): softmax [18912, 197] 7.07 -> 6.27 us on one MI355X.
-// Several rows per wave, all loads issued first, measured slower (2 rows
-// 6.57 us, 4 rows 7.75 us), as did staging blocks of rows through LDS with
-// 16-byte global accesses (11-15 us).
-template <typename T, int EPL>
-__global__ __launch_bounds__(256) void softmax_reg(RArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
-  const T* x = (const T*)a.x + row * a.ldx;
-  T* y = (T*)a.y + row * a.ldy;
-  float v[EPL];
-  float mx = -INFINITY;
+// Larger of two raw values (smaller with MIN); fp16 compares in fp16.
+template <bool MIN>
+__device__ __forceinline__ _Float16 pick(_Float16 a, _Float16 b) {
+  return MIN ? __builtin_fminf16(a, b) : __builtin_fmaxf16(a, b);
+}
+template <bool MIN>
+__device__ __forceinline__ __bf16 pick(__bf16 a, __bf16 b) {
+  return (MIN ? (float)b < (float)a : (float)b > (float)a) ? b : a;
+}
+
+// Row extremum over the G lanes of a row group: the largest raw value, or
+// the smallest with MIN.
+template <int G, bool MIN, typename T, int EPL>
+__device__ __forceinline__ float row_extremum(const T (&h)[EPL]) {
+  T m = h[0];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int c = lane + 64 * i;
-    v[i] = c < a.cols ? (float)x[c] * a.scale : -INFINITY;
-    mx = fmaxf(mx, v[i]);
-  }
-  mx = wave_max_dpp(mx);
+  for (int i = 1; i < EPL; ++i) m = pick<MIN>(m, h[i]);
+  const float f = (float)m;
+  return MIN ? -wave_reduce_dpp<G>(-f, [](float p, float q) { return fmaxf(p, q); })
+             : wave_reduce_dpp<G>(f, [](float p, float q) { return fmaxf(p, q); });
+}
+
+// One row per group of G lanes (64 / G rows per wave), EPL = ceil(cols / G)
+// elements per lane strided by G (coalesced 2-byte loads, any alignment):
+// every slot but the last lies inside the row, so only the last is masked.
+// The row extremum is taken on the raw values, since fp32 multiplication is
+// monotonic: max(s*x) = s*max(x) for s >= 0 and s*min(x) for s < 0.  Each
+// element then costs one fma for its exponent, 2^(x*s*log2e - m*s*log2e),
+// one v_exp_f32, one add and one multiply by the reciprocal of the row sum.
+// Softmax [18912, 197] on one MI355X: 3.97 us with 32 lanes per row (47 % of
+// HBM; 4.62 us with 64, 4.25 us with 16), against 5.76 us for one row per
+// wave with a scaled max and a divide; a plain 16-byte copy of the same
+// bytes takes 2.93 us.  Staging spans of rows through LDS with 16-byte
+// global accesses measured 6.4-9.3 us.
+template <typename T, int G, int EPL>
+__global__ __launch_bounds__(256) void softmax_rows(RArgs a) {
+  constexpr int RW = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave * RW >= a.rows) return;
+  const int64_t row = wave * RW + lane / G;
+  const bool ok = row < a.rows;  // lanes past the last row read it again and store nothing
+  const int c0 = lane % G;
+  const T* x = (const T*)a.x + (ok ? row : a.rows - 1) * a.ldx + c0;
+  const float sl2 = a.scale * 1.4426950408889634f;
+  const bool neg = sl2 < 0.f;
+  T h[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL - 1; ++i) h[i] = x[G * i];
+  const bool last = c0 + G * (EPL - 1) < a.cols;
+  // a masked slot repeats slot 0 (inside the row when EPL > 1) or, alone,
+  // holds a value that cannot win the extremum; it is left out of the sum
+  const T far = (T)(neg ? INFINITY : -INFINITY);
+  h[EPL - 1] = last ? x[G * (EPL - 1)] : (EPL > 1 ? h[0] : far);
+  const float m = neg ? row_extremum<G, true>(h) : row_extremum<G, false>(h);
+  const float nm = -(m * sl2);
+  float t[EPL];
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    const int c = lane + 64 * i;
-    v[i] = c < a.cols ? fast_exp(v[i] - mx) : 0.f;
-    sum += v[i];
+    t[i] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)h[i], sl2, nm));
+    if (i < EPL - 1 || last) sum += t[i];
   }
-  sum = wave_sum_dpp(sum);
-  const float inv = 1.0f / sum;
+  sum = wave_reduce_dpp<G>(sum, [](float p, float q) { return p + q; });
+  const float inv = __builtin_amdgcn_rcpf(sum);
+  if (!ok) return;
+  T* y = (T*)a.y + row * a.ldy + c0;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int c = lane + 64 * i;
-    if (c < a.cols) y[c] = (T)(v[i] * inv);
-  }
+  for (int i = 0; i < EPL - 1; ++i) y[G * i] = (T)(t[i] * inv);
+  if (last) y[G * (EPL - 1)] = (T)(t[EPL - 1] * inv);
 }
 
 // Wide rows: three passes (max, sum, write), re-reading x from cache.
@@ -190,17 +224,28 @@ hipError_t rms_launch(const RowProblem& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// softmax_rows<T, G, E> for E = epl (exactly), searched from E down to LO.
+template <typename T, int G, int E, int LO>
+bool softmax_rows_launch(const RArgs& a, int epl, hipStream_t stream) {
+  if constexpr (E < LO) {
+    return false;
+  } else {
+    if (epl != E) return softmax_rows_launch<T, G, E - 1, LO>(a, epl, stream);
+    const int64_t waves = (a.rows + 64 / G - 1) / (64 / G);
+    hipLaunchKernelGGL((softmax_rows<T, G, E>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, a);
+    return true;
+  }
+}
+
 template <typename T>
 hipError_t softmax_launch(const RowProblem& p, hipStream_t stream) {
   const RArgs a = make_args(p);
-  const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
-  const int64_t epl = (p.cols + 63) / 64;
-  if (epl <= 1) hipLaunchKernelGGL((softmax_reg<T, 1>), grid, block, 0, stream, a);
-  else if (epl <= 2) hipLaunchKernelGGL((softmax_reg<T, 2>), grid, block, 0, stream, a);
-  else if (epl <= 4) hipLaunchKernelGGL((softmax_reg<T, 4>), grid, block, 0, stream, a);
-  else if (epl <= 8) hipLaunchKernelGGL((softmax_reg<T, 8>), grid, block, 0, stream, a);
-  else if (epl <= 16) hipLaunchKernelGGL((softmax_reg<T, 16>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((softmax_any<T>), grid, block, 0, stream, a);
+  // 32 lanes a row up to 512 columns, 64 up to 1024, then three passes
+  bool done = false;
+  if (p.cols <= 512) done = softmax_rows_launch<T, 32, 16, 1>(a, (int)((p.cols + 31) / 32), stream);
+  else if (p.cols <= 1024) done = softmax_rows_launch<T, 64, 16, 9>(a, (int)((p.cols + 63) / 64), stream);
+  if (!done)
+    hipLaunchKernelGGL((softmax_any<T>), dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -83,3 +83,54 @@ def test_softmax_bf16(pkg, dev):
     y = pkg.softmax(x.to(dev), 0.125)
     torch.cuda.synchronize()
     assert ref.max_rel_err(np32(y.cpu()), ref.softmax(np32(x), 0.125)) <= TOL
+
+
+def _softmax_widths():
+    # every elements-per-lane count of both lane groupings (32 lanes a row up
+    # to 512 columns, 64 up to 1024) at both ends, and the three-pass width
+    w = set()
+    for e in range(1, 17):
+        w.update({32 * e - 31, 32 * e})
+    for e in range(9, 17):
+        w.update({64 * e - 63, 64 * e})
+    return sorted(w | {1025})
+
+
+def test_softmax_every_lane_count(pkg, dev):
+    # odd row counts: the last wave's second row group is past the matrix
+    for i, cols in enumerate(_softmax_widths()):
+        rows = 3 + 2 * (i % 3)
+        x = normal((rows, cols), 100 + i)
+        y = np32(pkg.softmax(x.to(dev), 0.7).cpu())
+        want = ref.softmax(x.numpy(), 0.7)
+        assert ref.max_rel_err(y, want) <= TOL, cols
+        assert np.allclose(y.sum(-1), 1.0, atol=2e-3), cols
+
+
+@pytest.mark.parametrize("scale", [-0.3, 0.0, 0.125])
+def test_softmax_scale_sign_and_masked_entries(pkg, dev, scale):
+    # the row extremum is taken on the raw values: the smallest one for a
+    # negative scale; -inf entries (masked scores) get weight 0
+    x = normal((37, 197), 11)
+    if scale != 0.0:  # (inf * 0 is NaN)
+        x[::3, 5::7] = float("-inf") if scale > 0 else float("inf")
+    y = np32(pkg.softmax(x.to(dev), scale).cpu())
+    want = ref.softmax(x.numpy(), scale)
+    assert ref.max_rel_err(y, want) <= TOL
+    if scale != 0.0:
+        assert not np.any(y[::3, 5::7])
+    # a row with every entry masked is NaN, as in torch
+    z = torch.full((3, 40), float("-inf"), dtype=torch.float16)
+    z[1] = 0
+    yz = np32(pkg.softmax(z.to(dev), 1.0).cpu())
+    assert np.isnan(yz[0]).all() and np.isnan(yz[2]).all() and np.allclose(yz[1], 1 / 40, rtol=2 ** -10)
+
+
+def test_softmax_strided_rows(pkg, dev):
+    # leading dimensions past the row: padded score rows as attention keeps them
+    base = normal((19, 256), 12)
+    out = torch.full((19, 224), 5.0, dtype=torch.float16, device=dev)
+    y = pkg.softmax(base.to(dev)[:, :197], 0.125, out=out[:, :197])
+    got = np32(out.cpu())
+    assert ref.max_rel_err(np32(y.cpu()), ref.softmax(base[:, :197].numpy(), 0.125)) <= TOL
+    assert np.all(got[:, 197:] == 5.0)
