@@ -289,7 +289,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   constexpr int BNO = (EPI == EPI_SILU_MUL) ? BN / 2 : BN;
   constexpr int SROW = BNO * 2 + 16;
   constexpr int EPI_BYTES = OUTF32 ? 0 : BM * SROW;
-  constexpr int SMEM = (A_REGION + SBS * B_BYTES > EPI_BYTES) ? A_REGION + SBS * B_BYTES : EPI_BYTES;
+  constexpr int SMEM_OPS = (A_REGION + SBS * B_BYTES > EPI_BYTES) ? A_REGION + SBS * B_BYTES : EPI_BYTES;
+  // The epilogue's per-column vectors (bias, int8 scales) of the tile's BN
+  // columns sit after that, 1 KB each: one direct load by wave 0 at the
+  // start, so they cost no registers through the main loop and the
+  // epilogue (the 8-wave 256x256 tile holds 256 accumulator VGPRs a lane).
+  constexpr bool HAS_BIAS = EPI == EPI_BIAS || EPI == EPI_BIAS_GELU_TANH;
+  constexpr int NCV = (HAS_BIAS ? 1 : 0) + (BI8 ? 1 : 0);
+  constexpr int SMEM = SMEM_OPS + NCV * 1024;
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(STAGES >= 2 && STAGES <= 4, "STAGES");
   static_assert(SBS >= STAGES && SBS <= 8 && (!PP || SBS == STAGES), "B stages");
@@ -317,6 +324,33 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   const char* Bb = NN    ? a.B + (b * a.sB + (int64_t)n0) * 2
                    : BI8 ? a.B + (b * a.sB + (int64_t)n0 * a.ldb)
                          : a.B + (b * a.sB + (int64_t)n0 * a.ldb) * 2;
+
+  // column vectors -> LDS (N a multiple of 8: whole 16-byte chunks, columns
+  // past N read as zero); the prologue's first wait covers these loads, as
+  // they are issued before every operand load.  Other N read them from
+  // global memory in the epilogue.
+  static_assert(BN * 2 <= 1024, "column vector chunk");
+  const bool cv_lds = NCV > 0 && (a.N % 8) == 0;
+  char* const cv_bias = smem + SMEM_OPS;
+  char* const cv_scale = smem + SMEM_OPS + (HAS_BIAS ? 1024 : 0);
+  if (cv_lds && w == 0) {
+    const uint32_t off = (uint32_t)(n0 + lane * 8) * 2u;
+    if constexpr (HAS_BIAS) load_lds16(make_rsrc(a.bias, (uint32_t)a.N * 2u), (HXMI_LDS void*)to_lds(cv_bias), off);
+    if constexpr (BI8) load_lds16(make_rsrc(a.scale, (uint32_t)a.N * 2u), (HXMI_LDS void*)to_lds(cv_scale), off);
+  }
+  // 4 consecutive column-vector values starting at tile column nl (n0 + nl
+  // in the matrix)
+  auto colvec4 = [&](const char* cv, const char* gv, int nl, float* out) {
+    if (cv_lds) {
+      const short4v raw = *(const short4v*)(cv + nl * 2);
+      T t[4];
+      __builtin_memcpy(t, &raw, 8);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = (float)t[q];
+    } else {
+      load_bias4<T>(gv, n0 + nl, a.N, out);
+    }
+  };
 
   // ---- load plan --------------------------------------------------------------
   // Each wave instruction moves 1 KB (RPIK rows of a k-contiguous tile, or
@@ -696,13 +730,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
           for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * g + q] * alpha;
           if constexpr (BI8) {
             float sv[4];
-            load_bias4<T>(a.scale, n, a.N, sv);
+            colvec4(cv_scale, a.scale, n - n0, sv);
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] *= sv[q];
           }
-          if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU_TANH) {
+          if constexpr (HAS_BIAS) {
             float bv[4];
-            load_bias4<T>(a.bias, n, a.N, bv);
+            colvec4(cv_bias, a.bias, n - n0, bv);
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] += bv[q];
           }
@@ -751,13 +785,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
             for (int q = 0; q < 4; ++q) v[q] = acc[i][j][4 * g + q] * alpha;
             if constexpr (BI8) {
               float sv[4];
-              load_bias4<T>(a.scale, n0 + nl, a.N, sv);
+              colvec4(cv_scale, a.scale, nl, sv);
 #pragma unroll
               for (int q = 0; q < 4; ++q) v[q] *= sv[q];
             }
-            if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU_TANH) {
+            if constexpr (HAS_BIAS) {
               float bv[4];
-              load_bias4<T>(a.bias, n0 + nl, a.N, bv);
+              colvec4(cv_bias, a.bias, nl, bv);
 #pragma unroll
               for (int q = 0; q < 4; ++q) v[q] += bv[q];
             }

@@ -118,16 +118,21 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + fast_exp(-x)); }
+// x * sigmoid(x).  The quotient is x times v_rcp_f32 of the denominator
+// (within 1 ulp), not the IEEE division sequence (scale, fma chain, fixup),
+// which cost several times as much in the GEMM epilogues; either is far
+// inside the fp16 rounding of the result.  A denominator of +inf (x very
+// negative) gives rcp 0 and the result -0, as the quotient does.
+__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)); }
 
 // tanh-form GELU, 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))), evaluated as
 // x*sigmoid(2u) which equals it exactly in real arithmetic and avoids tanh's
-// cancellation near 0.
+// cancellation near 0 (the sigmoid's quotient as in silu).
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
   const float k1 = 0.044715f;
   float u = k0 * (x + k1 * x * x * x);
-  return x / (1.0f + fast_exp(-2.0f * u));
+  return x * __builtin_amdgcn_rcpf(1.0f + fast_exp(-2.0f * u));
 }
 
 template <typename T>
