@@ -227,8 +227,21 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 // With int8 weights the slices run 64x64 tiles (Qwen2.5-0.5B down
 // projection at M = 256: 105 -> 128 TFLOP/s).
 int gemm_splits(const GemmProblem& p) {
-  if (p.batch != 1 || p.out_f32 || p.rms || p.K < 2048 || p.K % 8 || !gemm_fast_path_ok(p)) return 1;
+  const bool i8 = p.dtype == DT_W8A16;
+  if (p.batch != 1 || p.out_f32 || p.rms || p.K < (i8 ? 512 : 2048) || p.K % 8 || !gemm_fast_path_ok(p)) return 1;
   if (const int64_t e = knob(KNOB_SPLITK); e != KNOB_UNSET) return e < 1 ? 1 : (e > 16 ? 16 : (int)e);
+  if (i8 && p.K < 2048) {
+    // int8 weights at short K with few output tiles (the Qwen2.5-0.5B
+    // 896 -> 896 projection at M = 256: 56 tiles of 64x64): each workgroup's
+    // K-steps wait on memory, so slices of >= 256 of K put the same steps on
+    // more CUs (10.7 -> 9.0 us with 3 slices; 7 slices of 128: 12.1 us)
+    const int64_t t64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+    if (t64 >= 128) return 1;
+    int s = (int)((240 + t64 / 2) / t64);
+    s = s < 1 ? 1 : (s > 4 ? 4 : s);
+    while (s > 1 && p.K / s < 256) --s;
+    return s;
+  }
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 127) / 128);
   if (tiles >= 384 || p.K < 3072) return 1;
   // long slices: two of them once every CU has a workgroup (measured in the
