@@ -444,15 +444,28 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   // substep s: the swizzle repeats every 16 rows and fragments start on
   // multiples of 32 rows, so it depends on the lane alone; the wave's first
   // row is folded in, leaving a constant per fragment (an immediate offset).
+  //
+  // Int8 B (BI8) is read 16 bytes (16 k) at a time, one chunk per pair of
+  // substeps: in substeps 2p and 2p+1 lane l (h = l / 32) takes k = 32p +
+  // 16h + 8(s & 1) .. +7 of its row, and its A fragment takes the same k
+  // (chunk 4p + 2h + (s & 1) instead of 2s + h).  An MFMA sums over
+  // whichever k its lanes hold as long as both operands agree, and the four
+  // substeps still cover k = 0..63 once.  The 16-byte read matters: after an
+  // 8-byte LDS read (the plain int8 fragment) the compiler waited for every
+  // outstanding direct-to-LDS load (vmcnt(0)), which drained the prefetch in
+  // every K-step.
   constexpr int SUBS_ = BK / 16;
-  uint32_t lofA[SUBS_], lofB[SUBS_];
+  uint32_t lofA[SUBS_], lofB[SUBS_], lofB8[SUBS_];
 #pragma unroll
   for (int s = 0; s < SUBS_; ++s) {
-    const int l = lane & 31;
-    const uint32_t o = (uint32_t)(l * RB + ((((s << 1) + (lane >> 5)) ^ kc_swz<RB>(l)) << 4));
-    lofA[s] = (uint32_t)(wm * WM * RB) + o;
-    lofB[s] = (uint32_t)(wn * WN * RB) + o;
+    const int l = lane & 31, h = lane >> 5;
+    const int ca = BI8 ? ((s >> 1) << 2) + (h << 1) + (s & 1) : (s << 1) + h;
+    lofA[s] = (uint32_t)(wm * WM * RB + l * RB + ((ca ^ kc_swz<RB>(l)) << 4));
+    lofB[s] = (uint32_t)(wn * WN * RB + l * RB + ((((s << 1) + h) ^ kc_swz<RB>(l)) << 4));
+    // int8 B rows (BK bytes) keep chunk c of row r at c ^ ((r >> 2) & 3)
+    lofB8[s] = (uint32_t)((wn * WN + l) * BK + (((2 * (s >> 1) + h) ^ ((l >> 2) & 3)) << 4));
   }
+  short8v fbo[BI8 ? TN : 1];  // BI8: the odd substep's B fragments, dequantised with the even one's
   // RAGGED (K % 8 != 0): the 16-byte chunk that straddles K brings in
   // elements past K (row padding, or the next row).  In the last K-step the
   // fragments keep only their elements below K; the NN B operand needs no
@@ -464,9 +477,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
       if constexpr (NN) {
         fb[i] = read_nn<BN>(sB_, wn * WN + i * 32, s, lane);
       } else if constexpr (BI8) {
-        // 8 int8 weights (row r, k = 16 s + 8 (lane / 32) ..) -> 8 fp16, exactly
-        const int r = wn * WN + i * 32 + (lane & 31);
-        fb[i] = dequant8(*(const int2v*)(sB_ + r * BK + ((s ^ ((r >> 2) & 3)) << 4) + (lane >> 5) * 8));
+        // 16 int8 weights of row wn WN + 32 i + lane % 32 -> 16 fp16,
+        // exactly, in the even substep: its fragment takes the first 8, the
+        // odd substep's the last 8
+        if ((s & 1) == 0) {
+          int4v q = __builtin_bit_cast(int4v, *(const short8v*)(sB_ + lofB8[s] + i * 32 * BK));
+          asm("" : "+v"(q));  // one 16-byte read, not two 8-byte ones
+          fb[i] = dequant8(int2v{q[0], q[1]});
+          fbo[i] = dequant8(int2v{q[2], q[3]});
+        } else {
+          fb[i] = fbo[i];
+        }
       } else {
         fb[i] = *(const short8v*)(sB_ + lofB[s] + i * 32 * RB);
       }
