@@ -604,15 +604,29 @@ def main() -> int:
         log("[bench] FAILED: the block's outputs differ from the fp32 reference by more than 1e-2")
         return 3
     if args.profile:
+        # gate/up back to back for --warmup-ms (steady clocks), then --steps
+        # launches timed with HIP events on the launch stream: the trace's
+        # last --steps dispatches are the ones the printed average covers
         step()
+        t_end = time.perf_counter() + args.warmup_ms * 1e-3
+        while time.perf_counter() < t_end:
+            for _ in range(10):
+                gate_up()
+            torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
         for _ in range(args.steps):
             gate_up()
+        e.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(e) * 1e3 / args.steps
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        log(f"[bench] profile mode: {args.steps} gate/up launches, 5 x 256 MiB copies")
+        log(f"[bench] profile mode: {args.steps} gate/up launches after {args.warmup_ms:.0f} ms of warm-up, "
+            f"{us:.2f} us each (HIP events), then 5 x 256 MiB copies")
         return 0
     # One step = the block's kernels launched eagerly on torch's current
     # stream (each kernel outlasts its host launch, so launches queue ahead of
