@@ -167,6 +167,26 @@ def test_gemm_epilogues(pkg, dev, force_tile, epi, tile):
     assert ref.max_rel_err(np32(c), exp) <= TOL
 
 
+@pytest.mark.parametrize("epi", ["bias", "bias_gelu_tanh"])
+@pytest.mark.parametrize("tile", [None, 3, 6, 8, 12])
+def test_gemm_bias_n_not_a_multiple_of_8(pkg, dev, force_tile, epi, tile):
+    """N % 8 != 0 with K % 8 == 0: the epilogue reads the bias from global
+    memory element by element instead of the per-tile LDS copy (which takes
+    whole 16-byte chunks); the padding columns of the output stay untouched."""
+    force_tile(tile)
+    M, N, K = 200, 93, 256
+    a = normal((M, K), 40)
+    w = normal((N, K), 41, 0.05)
+    bias = normal((N,), 42, 0.5)
+    outp = torch.full((M, 96), 7.0, dtype=torch.float16, device=dev)
+    pkg.gemm(a.to(dev), w.to(dev), b_layout="nt", epilogue=epi, bias=bias.to(dev), out=outp[:, :N])
+    torch.cuda.synchronize()
+    c = outp.cpu()
+    exp = ref.gemm_epilogue(a.numpy(), w.numpy(), "nt", epi, bias.numpy())
+    assert ref.max_rel_err(np32(c[:, :N]), exp) <= TOL
+    assert (c[:, N:] == 7.0).all()
+
+
 @pytest.mark.parametrize("tile", [None, 0, 1, 2, 3, 4, 11, 12, 13])
 def test_gemm_silu_mul(pkg, dev, force_tile, tile):
     force_tile(tile)

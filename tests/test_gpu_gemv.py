@@ -458,3 +458,37 @@ def test_gemv_bf16_exact_integers(pkg, dev):
     y = pkg.gemv(x.to(dev), w.to(dev)).cpu()
     exact = (x.double() @ w.double().T).to(torch.bfloat16)
     assert torch.equal(y, exact)
+
+
+@pytest.mark.parametrize("M", [64, 256])
+@pytest.mark.parametrize("N,K", [(264, 144), (520, 912), (4104, 208), (896, 848)])
+def test_w8a16_gemm_k_not_a_multiple_of_the_k_step(pkg, dev, M, N, K):
+    """The int8-weight MFMA GEMM (M > 16) reads each 16-byte chunk of int8
+    codes once per pair of 16-deep substeps; a K that ends inside a 64-deep
+    step leaves chunks past K, which must read as zero, in the last step.
+    (896x848 at M = 256 takes the short-K split path, slices of >= 256.)"""
+    x = normal((M, K), 61 + M)
+    q, s = int8_weights(N, K, 62)
+    b = normal((N,), 63)
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("tile", [None, 3, 4, 5, 6, 8, 12, 13])
+@pytest.mark.parametrize("splits", [None, 1, 3])
+def test_w8a16_gemm_integer_exact_every_tile(pkg, dev, tile, splits):
+    """Small-integer activations, int8 codes and unit scales: every fp32 sum
+    is exact, so each tile shape and K split must return the exactly rounded
+    product (the codes' k order in the paired reads must match the
+    activations' in every substep)."""
+    g = torch.Generator().manual_seed(64)
+    M, N, K = 96, 200, 784  # K % 64 = 16; K >= 512 so a K split applies
+    x = torch.randint(-3, 4, (M, K), generator=g).half()
+    q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = torch.ones(N, dtype=torch.float16)
+    with pkg.tuning(w8_tile=tile, splitk=splits):
+        y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev))
+        torch.cuda.synchronize()
+    exact = x.double() @ q.double().T
+    assert np.array_equal(y.cpu().numpy(), exact.numpy().astype(np.float16))
