@@ -146,13 +146,6 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
   const int kend = min(a.skv, wg_qlast + a.causal_off + 1);
   const int wkend = q0 < a.sq ? max(0, min(a.skv, min(q0 + 31, a.sq - 1) + a.causal_off + 1)) : 0;
 
-  // Q fragments of this wave's 32 queries (zero past the sequence)
-  short8v qf[DS];
-#pragma unroll
-  for (int s = 0; s < DS; ++s) {
-    qf[s] = short8v{};
-    if (qme < a.sq) qf[s] = *(const short8v*)(Q + ((int64_t)qme * a.ldq + s * 16 + h * 8) * 2);
-  }
   const _Float16* mrow = nullptr;
   if (MASK && qme < a.sq)
     mrow = (const _Float16*)a.mask + ((int64_t)(bh / a.mask_group) * a.bm + (int64_t)qme * a.ldm);
@@ -169,8 +162,7 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
   for (int t = 0; t < DT; ++t) oacc[t] = float16v{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int c0 = 0; c0 < kend; c0 += KC) {
-    if (c0 > 0) __syncthreads();  // previous chunk fully consumed
+  auto issue_chunk = [&](int c0) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int row = (i * NW + w) * (1024 / RB) + lr;
@@ -180,6 +172,25 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
       const uint32_t vo = live ? (uint32_t)(key * a.ldv * 2 + ((cs ^ v_swz<D>(row)) << 4)) : kOOB;
       load_lds16(rK, (HXMI_LDS void*)to_lds(ks + (i * NW + w) * 1024), ko);
       load_lds16(rV, (HXMI_LDS void*)to_lds(vs + (i * NW + w) * 1024), vo);
+    }
+  };
+  // The first chunk's K / V loads go out before the Q loads: the compiler
+  // waits for Q (which the chunk loop reads) before entering the loop, so
+  // Q issued first would put a whole memory round trip ahead of the K / V
+  // requests instead of the two overlapping.
+  if (kend > 0) issue_chunk(0);
+  // Q fragments of this wave's 32 queries (zero past the sequence)
+  short8v qf[DS];
+#pragma unroll
+  for (int s = 0; s < DS; ++s) {
+    qf[s] = short8v{};
+    if (qme < a.sq) qf[s] = *(const short8v*)(Q + ((int64_t)qme * a.ldq + s * 16 + h * 8) * 2);
+  }
+
+  for (int c0 = 0; c0 < kend; c0 += KC) {
+    if (c0 > 0) {
+      __syncthreads();  // previous chunk fully consumed
+      issue_chunk(c0);
     }
     wait_vmcnt0();
     __syncthreads();
