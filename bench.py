@@ -20,6 +20,7 @@ fp32) on the same block, on the host's allowed threads and on one thread.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import pathlib
@@ -358,6 +359,12 @@ def bench_decode_full(pkg, torch, dev, timer, iters):
         ms = timer.graph_ms(fn, iters)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    # the timed replays' own waits: an expired one voids the timing
+    torch.cuda.synchronize()
+    status = pkg.hxmi.decode_status()
+    if status != 0:
+        raise SystemExit(f"[bench] decode step: a wait expired during the timed graph replays (status {status})")
+    res["status_after_replays"] = status
     del st
     return res
 
@@ -412,6 +419,38 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def _host_cpu_info() -> dict:
+    """What lscpu reports (model name, sockets, cores per socket, threads per
+    core), the physical cores (distinct (package, core) pairs in
+    /proc/cpuinfo) and the logical CPUs this process may run on."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)"):
+                info["lscpu_" + key.lower().replace("(s)", "s").replace(" ", "_")] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    cores, pkg_id = set(), "0"
+    try:
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "physical id":
+                pkg_id = val.strip()
+            elif key == "core id":
+                cores.add((pkg_id, val.strip()))
+    except OSError:
+        pass
+    info["physical_cores"] = len(cores) or None
+    info["allowed_cpus"] = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return info
+
+
 def cpu_baseline(runs: int = 7) -> dict:
     """The reference's CPU path for the headline block: PyTorch CPU ops in
     fp32 (the x86 forward its benchmarks compare against,
@@ -463,7 +502,7 @@ def cpu_baseline(runs: int = 7) -> dict:
                       f"TinyLlama block (RMSNorm, QKV, O, gate/up + SiLU-mul, down), median of {runs} blocks "
                       f"after a warm-up, {ms_all:.1f} ms each on {all_threads} threads",
             "median_ms": round(ms_all, 2), "single_thread": {"value": tf(ms_one), "median_ms": round(ms_one, 2)},
-            "cpu_model": _cpu_model(), "host_cpus": os.cpu_count(), "torch": torch.__version__}
+            "cpu_model": _cpu_model(), "host_cpus": os.cpu_count(), **_host_cpu_info(), "torch": torch.__version__}
 
 
 def profile_suite(pkg, torch, dev, timer) -> None:
@@ -553,6 +592,17 @@ def traffic_from_profiles():
     return None
 
 
+def teardown(torch, pkg) -> None:
+    """Finish the GPU work and release the library's cached workspaces and
+    torch's cached blocks before the interpreter exits, so that no device
+    memory the kernels used is still held while the runtime unloads."""
+    torch.cuda.synchronize()
+    pkg.hxmi.release_workspaces()
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -586,7 +636,13 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     timer = Timer(torch)
+    try:
+        return run(args, pkg, torch, dev, timer)
+    finally:
+        teardown(torch, pkg)
 
+
+def run(args, pkg, torch, dev, timer) -> int:
     if args.profile_suite:
         profile_suite(pkg, torch, dev, timer)
         return 0

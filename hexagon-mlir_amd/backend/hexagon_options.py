@@ -25,8 +25,10 @@ but have no GPU meaning; they affected Hexagon code generation only):
       gate/up packing) are written to <func>.constants.safetensors in the
       run's artifact folder and read back from there before the run.
   enableLWP
-      Per-op timing (HIP events around every node) written to lwp.json in the
-      run's artifact folder, the GPU analogue of the light-weight profiler.
+      Per-op timing in the light-weight profiler's format: a kernel enqueued
+      before and after every planned op stamps the GPU's wall clock into a
+      record buffer, written to lwp.json ({"entries": [{"id", "cyc"}]},
+      begin/end pairs per op id) in the run's artifact folder.
 """
 import hashlib
 import os

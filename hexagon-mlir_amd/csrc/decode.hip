@@ -12,7 +12,7 @@
 // do not depend on the data: the step is a chain of 4L dependent,
 // latency-bound phases over 0.7 GB of weights (Qwen2.5-0.5B).
 //
-// One cooperative launch keeps one workgroup per CU for the whole chain.
+// One launch keeps one workgroup per CU (at most) for the whole chain.
 //   * Loader waves stream the workgroup's rows of every layer's weights, in
 //     phase order, through a 128 KiB LDS ring with direct global->LDS loads,
 //     up to the ring's size ahead of the data dependencies.  A loader issues
@@ -110,7 +110,10 @@ struct Shared {
   _Float16 ain[kPI * 512];  // SiLU-mul output
   _Float16 vin[kMaxKV];     // v
   _Float16 hin[kPH * 512];  // B operand: normalised X / X1, or the attention output
-  float red[2][kMaxTiles * kNC][16];  // K-split partial row sums
+  // K-split partial row sums, one set per phase parity: a wave writes the
+  // set of phase p + 2 only after the rendezvous of phase p + 1, which every
+  // wave reaches after it has read its tiles of phase p
+  float red[2][kMaxTiles * kNC][16];
   int prog[kNC];            // per compute wave: every row it owns that starts below this byte is done
   int filled[kNL];          // per loader: batches completed
   int sync_cnt;
@@ -587,30 +590,32 @@ __device__ __forceinline__ float own_row(float4v acc, int c) {
   return c == 0 ? acc[0] : c == 1 ? acc[1] : c == 2 ? acc[2] : acc[3];
 }
 
-// Sum of the K-parts of tile row r in red[buf] (parts 0..kp-1 at unit base..).
-__device__ __forceinline__ float part_sum(const Shared& s, int buf, int base, int kp, int r) {
+// Sum of the K-parts of tile row r in red[par] (parts 0..kp-1 at unit base..).
+__device__ __forceinline__ float part_sum(const Shared& s, int par, int base, int kp, int r) {
   float v = 0.f;
-  for (int p = 0; p < kp; ++p) v += s.red[buf][base + p][r];
+  for (int p = 0; p < kp; ++p) v += s.red[par][base + p][r];
   return v;
 }
 
 // Runs a phase for wave w and hands each finished row to out(m, v, 0)
 // (stream row m, fp32 sum) on one lane; with pairs, out(i, gate, up) gets
 // pair i (stream rows 2i, 2i+1).  Waits for the ring data of each tile and
-// releases ring bytes as described at Plan.  false: gave up.
+// releases ring bytes as described at Plan.  The K-parts meet in
+// s.red[par] (par: the phase's parity); a large phase alternates two groups
+// of kNC units tile by tile.  false: gave up.
 template <bool PAIRS, typename Out>
-__device__ __forceinline__ bool run_phase(Shared& s, const Plan& pl, int sp, int end, int nr, int rb, int swz, int K,
-                                          const _Float16* hsrc, int w, int lane, int& nsync, const Guard& gd,
+__device__ __forceinline__ bool run_phase(Shared& s, const Plan& pl, int par, int sp, int end, int nr, int rb, int swz,
+                                          int K, const _Float16* hsrc, int w, int lane, int& nsync, const Guard& gd,
                                           Out out) {
   const int c = lane & 15, g4 = lane >> 4;
   const int k0 = w * pl.steps / pl.kp, k1 = (w + 1) * pl.steps / pl.kp;  // this wave's K-part
-  // finishes tile `tile` (rows m0.., n of them) from the K-parts in red[buf][base..]
-  auto finish = [&](int buf, int base, int m0, int n) {
+  // finishes a tile (rows m0.., n of them) from the K-parts in red[par][base..]
+  auto finish = [&](int base, int m0, int n) {
     if (PAIRS) {
       if (2 * lane + 1 < n)
-        out(m0 / 2 + lane, part_sum(s, buf, base, pl.kp, 2 * lane), part_sum(s, buf, base, pl.kp, 2 * lane + 1));
+        out(m0 / 2 + lane, part_sum(s, par, base, pl.kp, 2 * lane), part_sum(s, par, base, pl.kp, 2 * lane + 1));
     } else if (lane < n) {
-      out(m0 + lane, part_sum(s, buf, base, pl.kp, lane), 0.f);
+      out(m0 + lane, part_sum(s, par, base, pl.kp, lane), 0.f);
     }
   };
   for (int tile = 0; tile < pl.tiles; ++tile) {
@@ -618,20 +623,20 @@ __device__ __forceinline__ bool run_phase(Shared& s, const Plan& pl, int sp, int
     if (w < pl.kp) {
       if (!wait_fill(s, sp + (m0 + n) * rb, gd)) return false;
       const float4v acc = tile_dot(s, sp, rb, swz, m0, n, K >> 3, k0, k1, hsrc, lane);
-      if (c < 4) s.red[pl.seq ? tile & 1 : 0][(pl.seq ? 0 : tile * pl.kp) + w][4 * g4 + c] = own_row(acc, c);
+      if (c < 4) s.red[par][(pl.seq ? (tile & 1) * kNC : tile * pl.kp) + w][4 * g4 + c] = own_row(acc, c);
     }
     if (pl.seq) {
       cfence();
       if (lane == 0) lds_st(&s.prog[w], tile + 1 < pl.tiles ? sp + (m0 + 16) * rb : end);
       if (!sync_compute(s, nsync, gd)) return false;
-      if (tile % kNC == w) finish(tile & 1, 0, m0, n);
+      if (tile % kNC == w) finish((tile & 1) * kNC, m0, n);
     }
   }
   if (pl.seq) return true;
   cfence();
   if (lane == 0) lds_st(&s.prog[w], end);
   if (!sync_compute(s, nsync, gd)) return false;
-  for (int tile = w; tile < pl.tiles; tile += kNC) finish(0, tile * pl.kp, tile * 16, min(16, nr - tile * 16));
+  for (int tile = w; tile < pl.tiles; tile += kNC) finish(tile * pl.kp, tile * 16, min(16, nr - tile * 16));
   return true;
 }
 
@@ -669,7 +674,7 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
       weight_pieces(a.g_attn + (int64_t)l * rbH, kh, lane, gw);
       if (!poll_shared(a, XBc, l == 0 ? a.x : nullptr, H, tag, s.xin, w, s, nsync, gd)) return;
       norm_part(s, H, a.eps, kh, lane, gw);
-      const bool ok = run_phase<false>(s, p0, sl, sl + g.pre1, g.rows0, rbH, a.swzH, H, s.hin, w, lane, nsync, gd,
+      const bool ok = run_phase<false>(s, p0, 0, sl, sl + g.pre1, g.rows0, rbH, a.swzH, H, s.hin, w, lane, nsync, gd,
                                        [&](int m, float v, float) {
         const int row = g.row00 + m;
         if (a.b_qkv) v += (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + row];
@@ -684,7 +689,7 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
     {
       if (!poll_shared(a, VBc, nullptr, NKV, tag, s.vin, w, s, nsync, gd)) return;
       attn_part(s, a.HD, a.grp, kh, lane);
-      const bool ok = run_phase<false>(s, p1, sl + g.pre1, sl + g.pre2, g.rows1, rbH, a.swzH, H, s.hin, w, lane,
+      const bool ok = run_phase<false>(s, p1, 1, sl + g.pre1, sl + g.pre2, g.rows1, rbH, a.swzH, H, s.hin, w, lane,
                                        nsync, gd, [&](int m, float v, float) {
         const int row = g.row01 + m;
         const _Float16 x1 = (_Float16)((float)s.xin[row] + (float)(_Float16)v);
@@ -698,7 +703,7 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
       weight_pieces(a.g_mlp + (int64_t)l * rbH, kh, lane, gw);
       if (!poll_shared(a, X1Bc, nullptr, H, tag, s.xin, w, s, nsync, gd)) return;
       norm_part(s, H, a.eps, kh, lane, gw);
-      const bool ok = run_phase<true>(s, p2, sl + g.pre2, sl + g.pre3, g.rows2, rbH, a.swzH, H, s.hin, w, lane,
+      const bool ok = run_phase<true>(s, p2, 0, sl + g.pre2, sl + g.pre3, g.rows2, rbH, a.swzH, H, s.hin, w, lane,
                                       nsync, gd, [&](int i, float gv, float uv) {
         const _Float16 gh = (_Float16)gv, uh = (_Float16)uv;
         const _Float16 sh = (_Float16)silu((float)gh);
@@ -712,7 +717,7 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
     {
       // only this wave's K-part of the SiLU-mul output (pieces are 2 groups of 4 words)
       if (!poll_vector(a, ABc, I, 2 * ki.q0, 2 * ki.q1, tag, s.ain, gd)) return;
-      const bool ok = run_phase<false>(s, p3, sl + g.pre3, sl + g.pre4, g.rows3, rbI, a.swzI, I, s.ain, w, lane,
+      const bool ok = run_phase<false>(s, p3, 1, sl + g.pre3, sl + g.pre4, g.rows3, rbI, a.swzI, I, s.ain, w, lane,
                                        nsync, gd, [&](int m, float v, float) {
         const int row = g.row03 + m;
         const _Float16 xn = (_Float16)((float)s.xin[row] + (float)(_Float16)v);
@@ -764,11 +769,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_step_persistent(DArgs a) {
 
 int rup64(int64_t n) { return (int)((n + 63) / 64 * 64); }
 
-struct DevInfo {
-  int cus = 0;
-  int coop = 0;
-};
-
 }  // namespace
 
 bool decode_shape_ok(int64_t H, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t I) {
@@ -806,15 +806,20 @@ hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  int cus = 0, coop = 0;
+  int cus = 0;
   if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-  if ((e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev)) != hipSuccess) return e;
   int per_cu = 0;
   if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_persistent, kThreads, 0)) !=
       hipSuccess)
     return e;
-  if (!coop || per_cu < 1 || cus < 1) return hipErrorNotSupported;
-  if (!decode_grid_ok(p.H, p.kv_heads * p.head_dim, p.I, p.L, cus)) return hipErrorNotSupported;
+  if (per_cu < 1 || cus < 1) return hipErrorNotSupported;
+  // At most one workgroup per CU, and no more than H or I: then every
+  // workgroup owns rows in every phase, so every phase's output needs every
+  // workgroup, and no workgroup can run a phase ahead of one still polling
+  // the vector it would overwrite (a published vector is rewritten one
+  // layer later, after a phase that waited for that poller's own rows).
+  const int G = (int)std::min<int64_t>(cus, std::min(p.H, p.I));
+  if (!decode_grid_ok(p.H, p.kv_heads * p.head_dim, p.I, p.L, G)) return hipErrorNotSupported;
 
   DArgs a{};
   a.x = (const char*)p.x;
@@ -851,9 +856,13 @@ hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream) {
   a.swzH = swz(p.H);
   a.swzI = swz(p.I);
   a.timeout = (uint64_t)(p.timeout_us > 0 ? p.timeout_us : 1000000) * 100;  // 100 MHz clock
-  void* args[] = {&a};
-  return hipLaunchCooperativeKernel((const void*)decode_step_persistent, dim3(cus), dim3(kThreads), args, 0,
-                                    stream);
+  // An ordinary launch: G <= the CU count workgroups, each of which fits a
+  // CU on its own, are all resident at once on a device with nothing else
+  // running.  Should some not be (another stream's kernel holding CUs), the
+  // resident ones wait for them with bounded waits, so the launch ends with
+  // the error word set rather than hanging.
+  hipLaunchKernelGGL(decode_step_persistent, dim3(G), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
 }
 
 }  // namespace hxmi

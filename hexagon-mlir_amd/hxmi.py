@@ -174,26 +174,80 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-_WS_CACHE: "collections.OrderedDict[tuple[int, int], torch.Tensor]" = collections.OrderedDict()
-_WS_KEEP = 16  # workspaces kept (one per device and stream, least recently used dropped)
+_WS_CACHE: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
+_WS_KEEP = 16  # workspaces kept (one per device and stream or capture, least recently used dropped)
+# Counter head of a split-K workspace (kWsCounterBytes in csrc/hxmi_internal.h):
+# the only part that must be zero when a call starts.
+_WS_COUNTER_BYTES = 16 * 1024
+
+_hip_rt: Optional[ctypes.CDLL] = None
+
+
+def _hip_runtime() -> Optional[ctypes.CDLL]:
+    """The HIP runtime torch has loaded (for hipStreamGetCaptureInfo), or None."""
+    global _hip_rt
+    if _hip_rt is None:
+        for cand in (pathlib.Path(torch.__file__).parent / "lib" / "libamdhip64.so", "libamdhip64.so"):
+            try:
+                rt = ctypes.CDLL(str(cand))
+            except OSError:
+                continue
+            fn = rt.hipStreamGetCaptureInfo
+            fn.argtypes = [_P, ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_ulonglong)]
+            fn.restype = _I
+            _hip_rt = rt
+            break
+    return _hip_rt
+
+
+def _capture_key(device: torch.device) -> Optional[tuple]:
+    """None when the current stream of `device` is not capturing a HIP graph;
+    else a key unique to the capture under way (its capture id), or a fresh
+    object when the id cannot be read (nothing is then shared between calls)."""
+    if not torch.cuda.is_current_stream_capturing():
+        return None
+    rt = _hip_runtime()
+    if rt is not None:
+        status, cid = _I(0), ctypes.c_ulonglong(0)
+        stream = torch.cuda.current_stream(device).cuda_stream
+        if rt.hipStreamGetCaptureInfo(stream, ctypes.byref(status), ctypes.byref(cid)) == 0 and status.value == 1:
+            return ("capture", cid.value)
+    return ("capture", object())
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def _workspace(nbytes: int, device: torch.device) -> Optional[torch.Tensor]:
-    """Split-K scratch for the current stream of `device`.  The C ABI wants the
-    arrival counters at its head zero when a call starts and leaves them zero
-    afterwards, so one zero-filled buffer per (device, stream) serves every
-    call on that stream; it is replaced by a larger zero-filled one when a call
-    needs more.  Allocated on that stream, a dropped buffer is handed out
-    again by torch's caching allocator only in that stream's order, after the
-    kernels that used it; calls on different streams never share one."""
+    """Split-K scratch for the calls launched on the current stream of `device`.
+
+    The C ABI wants the arrival counters at the workspace's head zero when a
+    call starts and leaves them zero afterwards, so one buffer whose counters
+    were cleared before its first call serves every later call in the same
+    stream order.  Eager calls share one buffer per (device, stream),
+    replaced by a larger one when a call needs more; allocated on that
+    stream, a dropped buffer is handed out again by torch's caching allocator
+    only in that stream's order.
+
+    Inside a HIP graph capture nothing is run, only recorded, so the clearing
+    fill of a buffer belongs to the graph that captured it.  Each capture
+    therefore gets buffers of its own (keyed by its capture id, from the
+    graph's memory pool), cleared by a fill node recorded before their first
+    use: every replay of that graph clears them again, and no other graph or
+    eager call ever sees them.  Two graphs replayed concurrently thus never
+    share counters, whatever order they are captured or replayed in."""
     if nbytes <= 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           _raw_stream(device.index) if _raw_stream is not None else torch.cuda.current_stream(device).cuda_stream)
+    cap = _capture_key(device)
+    stream = (_raw_stream(device.index) if _raw_stream is not None
+              else torch.cuda.current_stream(device).cuda_stream)
+    key = (_device_index(device), stream if cap is None else cap)
     ws = _WS_CACHE.get(key)
     if ws is None or ws.numel() * 4 < nbytes:
-        # torch.zeros clears with a fill kernel, which is also safe inside graph capture
-        ws = torch.zeros((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+        ws = torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+        # a fill kernel (recorded as a kernel node under capture), counters only
+        ws[: min(ws.numel(), _WS_COUNTER_BYTES // 4)].zero_()
         _WS_CACHE[key] = ws
     _WS_CACHE.move_to_end(key)
     while len(_WS_CACHE) > _WS_KEEP:
@@ -620,24 +674,28 @@ class DecoderStack:
         return L, H, self.w_gu.shape[1] // 2, (nqkv - H) // 2
 
 
-_DECODE_WS: "dict[tuple, torch.Tensor]" = {}
-
-
-def _decode_key(device: torch.device, shape: tuple) -> tuple:
-    return (device.index if device.index is not None else torch.cuda.current_device(),
-            torch.cuda.current_stream(device).cuda_stream, shape)
+_DECODE_WS: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
+_DECODE_KEEP_CAPTURED = 32  # workspaces of captured graphs kept for decode_status (oldest dropped)
 
 
 def _decode_workspace(device: torch.device, shape: tuple, nbytes: int) -> torch.Tensor:
-    """The decode workspace of the current stream of `device` for one stack
-    shape (hidden, kv_dim, intermediate): it carries the step's published
-    vectors and running tag from call to call, so it is kept (zero-filled
-    when created) and shared neither between streams nor between shapes."""
-    key = _decode_key(device, shape)
+    """The decode workspace for one stack shape (hidden, kv_dim, intermediate)
+    of the calls launched on the current stream of `device`: it carries the
+    step's published vectors and running tag from call to call, so it is
+    kept, zero-filled when created, and shared neither between streams nor
+    between shapes.  Inside a HIP graph capture each capture gets its own
+    (keyed by its capture id), zero-filled by a fill node recorded before its
+    first use, so every replay starts from the zero state and no other graph
+    or eager call touches it."""
+    cap = _capture_key(device)
+    key = (_device_index(device), torch.cuda.current_stream(device).cuda_stream if cap is None else cap, shape)
     ws = _DECODE_WS.get(key)
     if ws is None:
         ws = torch.zeros((nbytes + 255) // 256 * 64, dtype=torch.int32, device=device)
         _DECODE_WS[key] = ws
+        captured = [k for k in _DECODE_WS if isinstance(k[1], tuple)]
+        for k in captured[: max(0, len(captured) - _DECODE_KEEP_CAPTURED)]:
+            del _DECODE_WS[k]
     return ws
 
 
@@ -689,19 +747,29 @@ def decode_step(x: torch.Tensor, stack: DecoderStack, *, out_qkv: bool = False,
 
 
 def decode_status(device: Optional[torch.device] = None, clear: bool = True) -> int:
-    """Error words of the current stream's decode workspaces after their work
-    has finished: 0 = every decode_step so far completed its waits, 1 = a
-    wait expired (that launch's outputs are undefined).  clear resets them."""
+    """Error words of the decode workspaces after their work has finished: 0 =
+    every decode_step so far completed its waits, 1 = a wait expired (that
+    launch's outputs are undefined).  It reads the workspaces of the current
+    stream's eager calls and those of every HIP graph captured on the device
+    (a graph's replays may run on any stream; its workspace holds the last
+    replay's word).  clear resets them."""
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
     stream = torch.cuda.current_stream(device).cuda_stream
-    dev_index = device.index if device.index is not None else torch.cuda.current_device()
+    dev_index = _device_index(device)
     status = 0
-    for (d, s, _), ws in _DECODE_WS.items():
-        if d == dev_index and s == stream:
+    for (d, s, _), ws in list(_DECODE_WS.items()):
+        if d == dev_index and (s == stream or isinstance(s, tuple)):
             st = ctypes.c_int(0)
             _check(load_library().hxmi_decode_status(ws.data_ptr(), int(clear), ctypes.byref(st), stream))
             status |= st.value
     return status
+
+
+def release_workspaces() -> None:
+    """Drop every cached split-K and decode workspace (after the work that
+    used them has finished), e.g. before the process tears the GPU state down."""
+    _WS_CACHE.clear()
+    _DECODE_WS.clear()
 
 
 def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:

@@ -323,7 +323,7 @@ int hxmi_attention_ex_f16(const void* q, const void* k, const void* v, void* o, 
 /*
  * One-token decoder step of a Llama / Qwen2 stack of `layers` layers at
  * position 0 (empty KV cache), fp16 in and out, fp32 accumulation, as ONE
- * persistent cooperative launch (plus the lm_head GEMV when w_lm is given):
+ * persistent launch (plus the lm_head GEMV when w_lm is given):
  *   x_0 = x; for each layer l:
  *     h   = rmsnorm(x_l, g_attn[l]);   qkv = h . w_qkv[l]^T (+ b_qkv[l])
  *     att = attention of the single token: query head i gets v of key/value

@@ -6,10 +6,11 @@ import numpy as np
 import pytest
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from gpu_util import TOL, normal, np32, uniform
 from oracle import hot_path as ref
-from test_backend import Block, QKVIn, block_inputs, fold_lwp
+from test_backend import RMS, Block, QKVIn, block_inputs, fold_lwp
 
 pytestmark = pytest.mark.gpu
 
@@ -167,3 +168,121 @@ def test_constants_in_separate_artifact(backend, dev, tmp_path):
     names = {k for k, _ in launcher.last_plan.module.named_buffers()}
     names |= {k for k, _ in launcher.last_plan.module.named_parameters()}
     assert keys == names and any("rmsfold" in k for k in keys)
+
+
+# ---- the launcher at the benchmark configs' sizes -------------------------------------------
+
+
+class TinyLlamaBlock(nn.Module):
+    """One LLaMA decoder layer at TinyLlama-1.1B's sizes (hidden 2048, 32
+    query heads / 4 key-value heads of 64, intermediate 5632) as HF writes
+    it: RMSNorm, q/k/v, causal grouped-query SDPA, o + residual, RMSNorm,
+    SiLU(gate) * up, down + residual (RoPE left out: it is elementwise work
+    outside the path)."""
+
+    def __init__(self, h=2048, heads=32, kv_heads=4, inter=5632):
+        super().__init__()
+        self.heads, self.kv_heads, self.hd = heads, kv_heads, h // heads
+        self.norm1, self.norm2 = RMS(h), RMS(h)
+        self.q = nn.Linear(h, h, bias=False)
+        self.k = nn.Linear(h, kv_heads * self.hd, bias=False)
+        self.v = nn.Linear(h, kv_heads * self.hd, bias=False)
+        self.o = nn.Linear(h, h, bias=False)
+        self.gate = nn.Linear(h, inter, bias=False)
+        self.up = nn.Linear(h, inter, bias=False)
+        self.down = nn.Linear(inter, h, bias=False)
+        for lin in (self.q, self.k, self.v, self.o, self.gate, self.up, self.down):
+            nn.init.normal_(lin.weight, std=0.02)
+
+    def forward(self, x):
+        S = x.shape[0]
+        hs = self.norm1(x)
+        q = self.q(hs).view(S, self.heads, self.hd).transpose(0, 1)
+        k = self.k(hs).view(S, self.kv_heads, self.hd).transpose(0, 1)
+        v = self.v(hs).view(S, self.kv_heads, self.hd).transpose(0, 1)
+        att = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+        x = x + self.o(att.transpose(0, 1).reshape(S, -1))
+        hs = self.norm2(x)
+        return x + self.down(F.silu(self.gate(hs)) * self.up(hs))
+
+
+def tinyllama_oracle(m, x):
+    """The same layer from the oracle's functions in fp32, each projection's
+    output rounded to fp16 as the fp16 forward stores it."""
+    w = lambda lin: lin.weight.detach().numpy()  # noqa: E731
+    r16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)  # noqa: E731
+    S, hd = x.shape[0], m.hd
+    xf = x.float().numpy()
+    hs = ref.rms_norm_hf(xf, m.norm1.weight.detach().numpy(), m.norm1.eps)
+    q, k, v = (r16(ref.linear(hs, w(lin))) for lin in (m.q, m.k, m.v))
+    q = q.reshape(S, m.heads, hd).transpose(1, 0, 2)
+    k = k.reshape(S, m.kv_heads, hd).transpose(1, 0, 2)
+    v = v.reshape(S, m.kv_heads, hd).transpose(1, 0, 2)
+    att = r16(ref.sdpa(q, k, v, 1.0 / np.sqrt(hd), causal=1, kv_group=m.heads // m.kv_heads))
+    x1 = r16(xf + r16(ref.linear(att.transpose(1, 0, 2).reshape(S, -1), w(m.o))))
+    hs2 = ref.rms_norm_hf(x1, m.norm2.weight.detach().numpy(), m.norm2.eps)
+    a = r16(ref.silu_mul_linear(hs2, w(m.gate), w(m.up)))
+    return x1 + r16(ref.linear(a, w(m.down)))
+
+
+class ViTBlock(nn.Module):
+    """ViT-B/16 attention + MLP at batch 8 (197 tokens, 12 heads of 64,
+    MLP 768 -> 3072 -> 768 with tanh-GELU): q/k/v are given, as in the
+    benchmark config; the MLP reads its own input."""
+
+    def __init__(self, e=768, f=3072):
+        super().__init__()
+        self.fc1 = nn.Linear(e, f)
+        self.fc2 = nn.Linear(f, e)
+        for lin in (self.fc1, self.fc2):
+            nn.init.normal_(lin.weight, std=0.02)
+            nn.init.normal_(lin.bias, std=0.02)
+
+    def forward(self, q, k, v, x):
+        att = F.scaled_dot_product_attention(q, k, v)
+        return att, self.fc2(F.gelu(self.fc1(x), approximate="tanh"))
+
+
+def test_launcher_at_config_sizes(backend, dev, tmp_path, capsys):
+    """A 512-token TinyLlama-shaped layer and the ViT-B/16 batch-8 block
+    through run_torch_mlir: the plan uses the fused kernels (RMSNorm folded
+    into the projections, SiLU-mul and GELU epilogues, fused attention) and
+    the outputs match the oracle's composition of the same layer."""
+    torch.manual_seed(0)
+    tl = TinyLlamaBlock().half()
+    x = torch.randn(512, 2048, generator=torch.Generator().manual_seed(7)).half()
+    path = str(tmp_path / "tinyllama.pt2")
+    backend.write_program_to_file(backend.export_program(tl, [x]), path)
+    launcher = backend.TorchMLIRHexagonLauncher()
+    out = launcher.run_torch_mlir(path, [x], "tinyllama", str(tmp_path), iterations=3)
+    pats = sorted(p for p, _ in launcher.last_plan.kernels)
+    print(f"[launcher] tinyllama plan {pats}", flush=True)
+    assert pats == ["attention", "linear", "linear", "rms_linear", "rms_linear", "rms_linear", "rms_silu_mul"]
+    want = tinyllama_oracle(tl.float(), x)
+    err = ref.max_err_vs_scale(np32(out[0]), want)
+    print(f"[launcher] tinyllama layer max err vs scale {err:.2e}, elementwise {ref.max_rel_err(np32(out[0]), want):.2e}",
+          flush=True)
+    assert err <= TOL
+
+    vit = ViTBlock().half()
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(8, 12, 197, 64, generator=g).half() for _ in range(3))
+    xv = torch.randn(8 * 197, 768, generator=g).half()
+    path = str(tmp_path / "vit.pt2")
+    backend.write_program_to_file(backend.export_program(vit, [q, k, v, xv]), path)
+    launcher = backend.TorchMLIRHexagonLauncher()
+    att, y = launcher.run_torch_mlir(path, [q, k, v, xv], "vit", str(tmp_path), iterations=3)
+    pats = sorted(p for p, _ in launcher.last_plan.kernels)
+    print(f"[launcher] vit plan {pats}", flush=True)
+    assert pats == ["attention", "linear", "linear_gelu"]
+    want_att = ref.sdpa(q.numpy(), k.numpy(), v.numpy(), 0.125)
+    assert ref.max_err_vs_scale(np32(att), want_att) <= TOL
+    vf = vit.float()
+    want_y = ref.linear(ref.gemm_epilogue(xv.float().numpy(), vf.fc1.weight.detach().numpy(), "nt", "bias_gelu_tanh",
+                                          vf.fc1.bias.detach().numpy()),
+                        vf.fc2.weight.detach().numpy(), vf.fc2.bias.detach().numpy())
+    assert ref.max_rel_err(np32(y), want_y) <= TOL
+    text = capsys.readouterr().out
+    perfs = [float(p) for p in re.findall(r"Perf:\s*([0-9]+(?:\.[0-9]+)?)", text)]
+    assert len(perfs) == 2 and all(p > 0 for p in perfs)
+    print(f"[launcher] Test_Info perf (us): tinyllama layer {perfs[0]}, vit block {perfs[1]}", flush=True)
