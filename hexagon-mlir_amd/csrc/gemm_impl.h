@@ -657,7 +657,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, v), rP, off, 0, kCoherent);
           }
       wait_vmcnt0();
-      __shared__ int is_last;
+      // The flag lives in the operand stages (all loads landed, no reads
+      // left): a second __shared__ variable would make the compiler tag
+      // every LDS access with per-variable alias scopes, and then wait for
+      // every direct-to-LDS load before each transposing fragment read.
+      int& is_last = *(int*)smem;
       __syncthreads();
       if (threadIdx.x == 0) {
         // every other slice of this tile has stored its partials once the

@@ -64,7 +64,13 @@ __device__ __forceinline__ HXMI_LDS char* to_lds(char* p) { return (HXMI_LDS cha
 // ds_read_b64_tr_b16: within each 16-lane group the 4x16 block of b16 values
 // addressed by the lanes (lane L supplies row L/4, columns 4*(L%4)..+3) is
 // returned transposed: lane i receives column i, rows 0..3.
-__device__ __forceinline__ short4v lds_read_tr16(const char* p) {
+// The pointer is __restrict__ so that the inlined read carries an alias
+// scope: without one the compiler puts an s_waitcnt vmcnt(0) before every
+// transposing read, draining each outstanding direct-to-LDS load (every
+// prefetched K-step of a GEMM pipeline), which it does not do before plain
+// LDS reads.  Callers order LDS reuse themselves, as for plain reads: a
+// stage is read only after the wait and barrier that follow its loads.
+__device__ __forceinline__ short4v lds_read_tr16(const char* __restrict__ p) {
   fp16x4_raw v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((HXMI_LDS fp16x4_raw*)(to_lds(const_cast<char*>(p))));
   return __builtin_bit_cast(short4v, v);
 }
