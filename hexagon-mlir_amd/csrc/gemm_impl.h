@@ -300,7 +300,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(STAGES >= 2 && STAGES <= 4, "STAGES");
   static_assert(SBS >= STAGES && SBS <= 8 && (!PP || SBS == STAGES), "B stages");
-  static_assert(SMEM <= 159 * 1024, "LDS budget (with the split-K flag)");
+  static_assert(SMEM <= 160 * 1024, "LDS budget");
   static_assert(BM % (RPIK * NW) == 0, "A tile rows per wave");
   static_assert(NN || BN % (RPIK * NW) == 0, "B tile rows per wave");
   static_assert(!BI8 || (!NN && BK == 64 && BN % (16 * NW) == 0), "int8 B: [N,K], BK 64, 16-row loads");

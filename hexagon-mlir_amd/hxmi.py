@@ -100,7 +100,7 @@ def _check(rc: int) -> None:
 
 
 TUNING_KNOBS = ("gemm_tile", "group_m", "splitk", "w8_tile", "gemv_path", "gemv_tpb", "gemv_ks", "gemv_kg",
-                "gemv_unr", "gemv_pair_wg")
+                "gemv_unr", "gemv_pair_wg", "attn_cfg")
 
 
 def set_tuning(name: str, value) -> Optional[int]:

@@ -62,7 +62,8 @@ int hxmi_version(void);
  * (value < 0 removes it).  Knobs: "gemm_tile" (forced GEMM tile id),
  * "group_m", "splitk", "w8_tile", "gemv_path" (0 16-row MFMA, 1 vector-ALU
  * rows, 2 whole-line pairs, 3 whole-line pairs with K split), "gemv_tpb",
- * "gemv_ks", "gemv_kg", "gemv_unr", "gemv_pair_wg".  A knob without a thread
+ * "gemv_ks", "gemv_kg", "gemv_unr", "gemv_pair_wg", "attn_cfg" (fused
+ * attention: 10 * query waves + key-split waves).  A knob without a thread
  * override takes the value of the environment variable HXMI_<NAME> read once
  * when the library loaded, else the library's own choice.  Knobs change how a
  * result is computed (tile, K split, kernel), not what it is.  *previous
