@@ -507,7 +507,7 @@ def cpu_baseline(runs: int = 7) -> dict:
 
 def profile_suite(pkg, torch, dev, timer) -> None:
     """Launches for counter runs, each warmed up by time, then 5 launches:
-    4096^3 NT GEMM, the Qwen2.5-0.5B lm_head fp16 / int8 GEMVs (M = 1, 16)
+    4096^3 NT and NN GEMMs, the 1024^3 NN GEMM, the Qwen2.5-0.5B lm_head fp16 / int8 GEMVs (M = 1, 16)
     and the int8 GEMM at M = 256 (weights rotate over copies so none is
     cache-resident), the ViT-B/16 batch-8 fused attention, fc1 and fc2,
     softmax [18912, 197], RMSNorm [512, 2048]; then five 256 MiB copies."""
@@ -519,6 +519,18 @@ def profile_suite(pkg, torch, dev, timer) -> None:
     timer._warm(gemm)
     for _ in range(5):
         gemm()
+    gemm_nn = lambda i=0: pkg.gemm(a, b, b_layout="nn", out=c)
+    timer._warm(gemm_nn)
+    for _ in range(5):
+        gemm_nn()
+    # the 1024^3 NN GEMM (C = A . B, uniform [-1, 1] operands)
+    a1 = (torch.rand(1024, 1024, generator=g) * 2 - 1).half().to(dev)
+    b1k = (torch.rand(1024, 1024, generator=g) * 2 - 1).half().to(dev)
+    c1 = torch.empty(1024, 1024, dtype=torch.float16, device=dev)
+    g1024 = lambda i=0: pkg.gemm(a1, b1k, b_layout="nn", out=c1)
+    timer._warm(g1024)
+    for _ in range(5):
+        g1024()
     H, V = 896, 151936
     ws = [torch.empty(V, H, dtype=torch.float16, device=dev).normal_(0, 0.02) for _ in range(3)]
     qs = [torch.randint(-127, 128, (V, H), dtype=torch.int8, device=dev) for _ in range(3)]
@@ -576,7 +588,7 @@ def profile_suite(pkg, torch, dev, timer) -> None:
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log("[bench] profile suite: 4096^3 GEMM, lm_head GEMV fp16 M=1/16, int8 M=1/16/256, ViT-B/16 attention / fc1 / "
+    log("[bench] profile suite: 4096^3 GEMM NT / NN, 1024^3 GEMM NN, lm_head GEMV fp16 M=1/16, int8 M=1/16/256, ViT-B/16 attention / fc1 / "
         "fc2, softmax [18912, 197], RMSNorm [512, 2048], 5 x 256 MiB copies")
 
 
@@ -616,9 +628,10 @@ def main() -> int:
                     help="for rocprofv3: run only the dominant kernel (gate/up SiLU-mul GEMM) --steps times, then a "
                          "256 MiB device copy 5 times (calibrates FETCH_SIZE/WRITE_SIZE), and exit")
     ap.add_argument("--profile-suite", action="store_true",
-                    help="for rocprofv3 counter runs: the 4096^3 fp16 NT GEMM and the lm_head decode GEMVs (fp16 "
-                         "M=1 and M=16, int8 M=1), each warmed up and then launched 5 times, then the 256 MiB copy "
-                         "calibration, and exit")
+                    help="for rocprofv3 counter runs: the 4096^3 fp16 NT and NN GEMMs, the 1024^3 NN GEMM, the "
+                         "lm_head decode GEMVs (fp16 M=1 and M=16, int8 M=1/16) and int8 GEMM (M=256), the ViT-B/16 "
+                         "attention / fc1 / fc2, softmax and RMSNorm, each warmed up and then launched 5 times, then "
+                         "the 256 MiB copy calibration, and exit")
     ap.add_argument("--profile-decode", action="store_true",
                     help="for rocprofv3: the full Qwen2.5-0.5B one-token forward, as the persistent decode kernel "
                          "and as separate launches, checked against each other and timed, and exit")
