@@ -362,13 +362,11 @@ class _Planner:
             q, k, v = (_val(x) for x in n.args[:3])
             scale = arg(6, "scale", None) or 1.0 / math.sqrt(q.shape[-1])
             gqa = k.shape[-3] != q.shape[-3]
-            # masked, causal and grouped-query SDPA need the fused kernel's shapes; the rest stays on torch
-            if (mask is not None or causal or gqa) and not (q.shape[-1] in (64, 128) and v.shape[-1] == q.shape[-1]
-                                                            and scale > 0):
-                continue
+            # (hx_attention takes every head dim and fp16 / bf16: the fused kernel where it applies, else the
+            # three steps with the masked softmax)
             if gqa and not arg(7, "enable_gqa", False):
                 continue
-            if mask is not None and _val(mask).dtype not in (torch.bool, torch.float16):
+            if mask is not None and _val(mask).dtype not in (torch.bool, torch.float16, torch.bfloat16):
                 continue
             self.replace(n, hx_attention, (n.args[0], n.args[1], n.args[2], float(scale), mask, int(causal)),
                          "attention")

@@ -355,6 +355,58 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
 }
 
 namespace {
+int softmax_masked_common(int dtype, const void* x, void* y, int64_t slices, int64_t s_q, int64_t s_kv, int64_t ldx,
+                          int64_t stride_x, int64_t ldy, int64_t stride_y, const void* mask, int64_t ldm,
+                          int64_t stride_m, int64_t mask_group, int causal, float scale, void* stream,
+                          const char* name) {
+  REQUIRE(slices >= 0 && s_q >= 0 && s_kv >= 0, "%s: negative size", name);
+  if (slices == 0 || s_q == 0 || s_kv == 0) return ok();
+  REQUIRE(x && y, "%s: null pointer", name);
+  REQUIRE(ldx >= s_kv && ldy >= s_kv, "%s: row stride smaller than s_kv", name);
+  REQUIRE(stride_x >= 0 && stride_y >= 0, "%s: negative slice stride", name);
+  REQUIRE(slices == 1 || (stride_x >= s_q * ldx && stride_y >= s_q * ldy), "%s: slices overlap", name);
+  REQUIRE(causal >= 0 && causal <= 2, "%s: causal must be 0, 1 or 2", name);
+  REQUIRE(s_q < (1ll << 31) && s_kv < (1ll << 31), "%s: s_q or s_kv too large", name);
+  if (mask) {
+    REQUIRE(ldm >= s_kv && stride_m >= 0 && mask_group >= 1, "%s: bad mask strides or group", name);
+    REQUIRE(al(mask, 2), "%s: mask must be 2-byte aligned", name);
+  }
+  hxmi::MaskedSoftmaxProblem p{};
+  p.x = x;
+  p.y = y;
+  p.mask = mask;
+  p.slices = slices;
+  p.s_q = s_q;
+  p.s_kv = s_kv;
+  p.ldx = ldx;
+  p.stride_x = stride_x;
+  p.ldy = ldy;
+  p.stride_y = stride_y;
+  p.ldm = mask ? ldm : 0;
+  p.stride_m = mask ? stride_m : 0;
+  p.mask_group = mask ? mask_group : 1;
+  p.causal = causal;
+  p.scale = scale;
+  p.dtype = dtype;
+  return from_hip(hxmi::launch_softmax_masked(p, (hipStream_t)stream), name);
+}
+}  // namespace
+
+int hxmi_softmax_masked_f16(const void* x, void* y, int64_t slices, int64_t s_q, int64_t s_kv, int64_t ldx,
+                            int64_t stride_x, int64_t ldy, int64_t stride_y, const void* mask, int64_t ldm,
+                            int64_t stride_m, int64_t mask_group, int causal, float scale, void* stream) {
+  return softmax_masked_common(hxmi::DT_F16, x, y, slices, s_q, s_kv, ldx, stride_x, ldy, stride_y, mask, ldm,
+                               stride_m, mask_group, causal, scale, stream, "hxmi_softmax_masked_f16");
+}
+
+int hxmi_softmax_masked_bf16(const void* x, void* y, int64_t slices, int64_t s_q, int64_t s_kv, int64_t ldx,
+                             int64_t stride_x, int64_t ldy, int64_t stride_y, const void* mask, int64_t ldm,
+                             int64_t stride_m, int64_t mask_group, int causal, float scale, void* stream) {
+  return softmax_masked_common(hxmi::DT_BF16, x, y, slices, s_q, s_kv, ldx, stride_x, ldy, stride_y, mask, ldm,
+                               stride_m, mask_group, causal, scale, stream, "hxmi_softmax_masked_bf16");
+}
+
+namespace {
 int attention_common(const char* name, const void* q, const void* k, const void* v, void* o, int64_t bh,
                      int64_t s_q, int64_t s_kv, int64_t d, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                      int64_t stride_q, int64_t stride_k, int64_t stride_v, int64_t stride_o, int64_t kv_group,

@@ -155,6 +155,21 @@ struct RowProblem {
 hipError_t launch_rmsnorm(const RowProblem& p, hipStream_t stream);
 hipError_t launch_softmax(const RowProblem& p, hipStream_t stream);
 
+// Softmax of attention scores with the mask operand and the causal rule:
+// slices of s_q rows of s_kv columns, slice i reads mask slice
+// i / mask_group (mask fp16 or null; stride_m 0 broadcasts).
+struct MaskedSoftmaxProblem {
+  const void* x;
+  void* y;
+  const void* mask;
+  int64_t slices, s_q, s_kv;
+  int64_t ldx, stride_x, ldy, stride_y, ldm, stride_m, mask_group;
+  int causal;  // 0 none, 1 key j > query r removed, 2 j > r + s_kv - s_q
+  float scale;
+  int dtype;
+};
+hipError_t launch_softmax_masked(const MaskedSoftmaxProblem& p, hipStream_t stream);
+
 struct AttnProblem {
   const void* q;  // [B*H, S, D]
   const void* k;  // [B*H / kv_group, SKV, D]

@@ -263,6 +263,84 @@ hipError_t launch_softmax(const RowProblem& p, hipStream_t stream) {
 
 namespace {
 
+// ---- masked softmax: the attention scores' softmax with the mask operand --
+// y[i][r] = softmax(scale * x[i][r] + M[i / mask_group][r] + causal(r, .)),
+// one wave per row, three passes (max, sum, write) re-reading the row from
+// cache.  It serves the composite attention path (any head dim, bf16),
+// where the scores are already materialised by the batched GEMM; the fused
+// kernel applies the same rule inside its key loop.
+struct MArgs {
+  const char* x;
+  char* y;
+  const _Float16* mask;
+  int64_t slices;
+  int sq, skv;
+  int64_t ldx, sx, ldy, sy, ldm, sm, mgroup;
+  int causal;
+  float scale;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_masked(MArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.slices * a.sq) return;
+  const int64_t i = row / a.sq;
+  const int r = (int)(row - i * a.sq);
+  const T* x = (const T*)a.x + i * a.sx + r * a.ldx;
+  T* y = (T*)a.y + i * a.sy + r * a.ldy;
+  const _Float16* m = a.mask ? a.mask + (i / a.mgroup) * a.sm + (int64_t)r * a.ldm : nullptr;
+  // keys past `lim` are removed by the causal rule
+  const int lim = a.causal == 1 ? r : a.causal == 2 ? r + a.skv - a.sq : a.skv;
+  auto score = [&](int c) {
+    float v = (float)x[c] * a.scale;
+    if (m) v += (float)m[c];
+    return c > lim ? -INFINITY : v;
+  };
+  float mx = -INFINITY;
+  for (int c = lane; c < a.skv; c += 64) mx = fmaxf(mx, score(c));
+  mx = wave_max_dpp(mx);
+  // a row with every key removed has mx = -inf: exp(-inf - -inf) is NaN, and
+  // so is the row, as the reference's max / exp / sum / div decomposition
+  float sum = 0.f;
+  for (int c = lane; c < a.skv; c += 64) sum += fast_exp(score(c) - mx);
+  sum = wave_sum_dpp(sum);
+  const float inv = 1.0f / sum;
+  for (int c = lane; c < a.skv; c += 64) y[c] = (T)(fast_exp(score(c) - mx) * inv);
+}
+
+}  // namespace
+
+hipError_t launch_softmax_masked(const MaskedSoftmaxProblem& p, hipStream_t stream) {
+  const int64_t rows = p.slices * p.s_q;
+  if (rows == 0 || p.s_kv == 0) return hipSuccess;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks >= (1ll << 31)) return hipErrorInvalidValue;
+  MArgs a;
+  a.x = (const char*)p.x;
+  a.y = (char*)p.y;
+  a.mask = (const _Float16*)p.mask;
+  a.slices = p.slices;
+  a.sq = (int)p.s_q;
+  a.skv = (int)p.s_kv;
+  a.ldx = p.ldx;
+  a.sx = p.stride_x;
+  a.ldy = p.ldy;
+  a.sy = p.stride_y;
+  a.ldm = p.ldm;
+  a.sm = p.stride_m;
+  a.mgroup = p.mask_group;
+  a.causal = p.causal;
+  a.scale = p.scale;
+  if (p.dtype == DT_BF16)
+    hipLaunchKernelGGL(softmax_masked<__bf16>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(softmax_masked<_Float16>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+namespace {
+
 template <typename T>
 __global__ __launch_bounds__(256) void fold_rms_weight(const T* W, const T* g, T* Wg, int64_t N, int64_t K,
                                                        int64_t ldw, int64_t ldwg) {

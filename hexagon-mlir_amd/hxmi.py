@@ -51,6 +51,8 @@ SIGNATURES = {
     "hxmi_rmsnorm_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_f16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
     "hxmi_softmax_bf16": ([_P, _P, _I64, _I64, _I64, _I64, _F, _P], _I),
+    "hxmi_softmax_masked_f16": ([_P, _P] + [_I64] * 7 + [_P, _I64, _I64, _I64, _I, _F, _P], _I),
+    "hxmi_softmax_masked_bf16": ([_P, _P] + [_I64] * 7 + [_P, _I64, _I64, _I64, _I, _F, _P], _I),
     "hxmi_attention_f16": ([_P, _P, _P, _P] + [_I64] * 12 + [_F, _P], _I),
     "hxmi_attention_ex_f16": ([_P, _P, _P, _P] + [_I64] * 13 + [_P, _I64, _I64, _I64, _I, _F, _P], _I),
     "hxmi_rmsnorm_linear_f16": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _F, _P, _P, _P], _I),
@@ -567,7 +569,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional
     (grouped-query attention: that many q heads per kv head).  mask: additive (or boolean keep) mask
     broadcastable to [..., S, S_kv]; causal: 1 masks keys after the query (torch's is_causal), 2 after
     query + S_kv - S.  fp16 with D in {64, 128} and scale > 0 runs the fused kernel (hxmi_attention_ex_f16);
-    other unmasked cases run the reference's three steps as bmm(Q, K^T) -> softmax -> bmm(P, V)."""
+    every other case (bf16, other head dims) runs the reference's three steps as bmm(Q, K^T) -> softmax
+    (with the mask and causal rule: hxmi_softmax_masked_*) -> bmm(P, V)."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
     S, D = q.shape[-2:]
@@ -610,20 +613,40 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional
                                                     q3.shape[0], S, Skv, D, ldq, ldk, ldv, ldo, bq, bk, bv, bo,
                                                     group, mp, ldm, sm, mg, int(causal), float(scale), _stream(q)))
         return out if out is not None else o.reshape(*lead, S, D)
-    if mask is not None or causal or group != 1:
-        raise HxmiError("masked, causal and grouped-query attention run on the fused kernel only "
-                        "(fp16, head dim 64 or 128, scale > 0)")
-    # S and P rows padded to a multiple of 8 keys, so both GEMMs (ragged N
-    # for Q.K^T, ragged K for P.V) run on the MFMA path; softmax in place
+    # The reference's three steps: bmm(Q, K^T) * scale -> (+ mask, causal)
+    # softmax -> bmm(P, V).  The query heads of one K/V head form one batch
+    # entry of group * S rows (q slices i = hkv * group + g are consecutive),
+    # so each K/V slice is read by one GEMM batch entry.  S and P rows are
+    # padded to a multiple of 8 keys, so both GEMMs (ragged N for Q.K^T,
+    # ragged K for P.V) run on the MFMA path; the softmax runs in place.
+    _require_gpu(q3, k3, v3, mask)
+    if q3.dtype not in (torch.float16, torch.bfloat16) or k3.dtype != q3.dtype or v3.dtype != q3.dtype:
+        raise HxmiError("attention takes fp16 or bf16 q, k, v of one dtype")
+    nq, dv = q3.shape[0], v.shape[-1]
+    if group > 1:
+        q3 = q3.contiguous().view(nq // group, group * S, D)
     skv8 = (Skv + 7) // 8 * 8
-    sbuf = torch.empty((q3.shape[0], S, skv8), dtype=q.dtype, device=q.device)
-    s = bgemm(q3, k3, b_layout="nt", alpha=scale, out=sbuf[..., :Skv])
-    p = softmax(s, out=s)
+    sbuf = torch.empty((nq, S, skv8), dtype=q.dtype, device=q.device)
+    s = bgemm(q3, k3, b_layout="nt", alpha=scale, out=sbuf.view(q3.shape[0], q3.shape[1], skv8)[..., :Skv])
+    if mask is None and not causal:
+        p = softmax(s, out=s)
+    else:
+        mp, ldm, sm, mg = 0, 0, 0, 1
+        if mask is not None:
+            m, ldm, sm, mg = _mask_slices(mask, lead, S, Skv)
+            mp = m.data_ptr()
+        fn = (load_library().hxmi_softmax_masked_f16 if q.dtype == torch.float16
+              else load_library().hxmi_softmax_masked_bf16)
+        _check(fn(sbuf.data_ptr(), sbuf.data_ptr(), nq, S, Skv, skv8, S * skv8, skv8, S * skv8, mp or None, ldm,
+                  sm, mg, int(causal), 1.0, _stream(q)))
+        p = s
     if out is not None:
-        bgemm(p, v3, b_layout="nn", out=out.view(-1, S, v.shape[-1]))
+        if out.shape != (*lead, S, dv) or out.dtype != q.dtype:
+            raise HxmiError(f"out must be {q.dtype} {(*lead, S, dv)}")
+        bgemm(p, v3, b_layout="nn", out=out.view(q3.shape[0], q3.shape[1], dv))
         return out
     o = bgemm(p, v3, b_layout="nn")
-    return o.reshape(*lead, S, v.shape[-1])
+    return o.reshape(*lead, S, dv)
 
 
 def hexkl_matmul(act: torch.Tensor, w: torch.Tensor) -> torch.Tensor:

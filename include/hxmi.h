@@ -219,6 +219,32 @@ int hxmi_softmax_bf16(const void* x, void* y, int64_t rows, int64_t cols, int64_
                       void* stream);
 
 /*
+ * The softmax step of attention with the reference's mask operand and the
+ * causal rule, over `slices` slices of s_q rows of s_kv scores (fp16 or
+ * bf16 x / y, in place allowed):
+ *   y[i][r][j] = softmax_j(scale * x[i][r][j] + M[i / mask_group][r][j] + C[r][j])
+ * C[r][j] = -inf when causal = 1 and j > r, or causal = 2 and j > r + s_kv - s_q
+ * (torch's is_causal and the bottom-right rule), else 0.  x / y: row stride
+ * ldx / ldy, slice stride stride_x / stride_y (elements).  mask: fp16
+ * additive, row stride ldm >= s_kv, slice stride stride_m (0 broadcasts one
+ * slice), mask_group consecutive slices per mask slice; NULL for none.  A
+ * row whose every score is -inf comes out NaN, as the reference's
+ * max / exp / sum / div decomposition gives.  With hxmi_bgemm_* before and
+ * after it, this is attention for any head dimension, bf16, grouped K/V
+ * heads (query heads of one K/V head as one batch entry of group * s_q rows)
+ * and masks, where the fused kernel does not apply.
+ * Replaces: the mask addition and softmax of the tm_tensor.attention lowering
+ * (LowerTmTensor.cpp:158-163 adds the mask to the scaled scores, :165-229
+ * the max / exp / sum / div over each row).
+ */
+int hxmi_softmax_masked_f16(const void* x, void* y, int64_t slices, int64_t s_q, int64_t s_kv, int64_t ldx,
+                            int64_t stride_x, int64_t ldy, int64_t stride_y, const void* mask, int64_t ldm,
+                            int64_t stride_m, int64_t mask_group, int causal, float scale, void* stream);
+int hxmi_softmax_masked_bf16(const void* x, void* y, int64_t slices, int64_t s_q, int64_t s_kv, int64_t ldx,
+                             int64_t stride_x, int64_t ldy, int64_t stride_y, const void* mask, int64_t ldm,
+                             int64_t stride_m, int64_t mask_group, int causal, float scale, void* stream);
+
+/*
  * RMSNorm folded into the linear layer that consumes it (LLaMA QKV and
  * gate/up projections):
  *   C[M,N'] = epilogue(rmsnorm(x) . W^T),  rmsnorm(x)[m,k] = x[m,k] * g[k] / sqrt(mean_k x[m,k]^2 + eps)

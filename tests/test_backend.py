@@ -238,7 +238,8 @@ def test_planner_matches_hot_path_patterns(backend, oracle_kernels):
 
 class MaskedAttn(nn.Module):
     """Decoder-style attention calls: a padding mask, a causal one over
-    grouped K/V heads, and one the fused kernel cannot take (head dim 8)."""
+    grouped K/V heads, and one the fused kernel cannot take (head dim 8),
+    which runs the three steps with the masked softmax."""
 
     def forward(self, q, k, v, kg, vg, m, q8, k8, v8, m8):
         a = F.scaled_dot_product_attention(q, k, v, attn_mask=m)
@@ -258,12 +259,13 @@ def test_planner_routes_masked_causal_gqa_attention(backend, oracle_kernels):
     args = [q, k, v, kg, vg, m, q8, k8, v8, m8]
     ep = backend.export_program(MaskedAttn(), args)
     plan = backend.plan_program(ep, torch.device("cpu"), fusion=True)
-    assert sorted(p for p, _ in plan.kernels) == ["attention", "attention"]
-    assert sum("scaled_dot" in t for t in plan.torch_ops) == 1  # head dim 8 with a mask stays on torch
-    a, b, _ = plan(*args)
+    assert sorted(p for p, _ in plan.kernels) == ["attention", "attention", "attention"]
+    assert not any("scaled_dot" in t for t in plan.torch_ops)
+    a, b, c = plan(*args)
     ex = lambda x: x.float().numpy()  # noqa: E731
     assert ref.max_err_vs_scale(ex(a), ref.sdpa(ex(q), ex(k), ex(v), mask=ex(m))) < 1e-2
     assert ref.max_err_vs_scale(ex(b), ref.sdpa(ex(q), ex(kg), ex(vg), causal=1, kv_group=2)) < 1e-2
+    assert ref.max_err_vs_scale(ex(c), ref.sdpa(ex(q8), ex(k8), ex(v8), mask=ex(m8))) < 1e-2
 
 
 def test_planner_without_fusion_keeps_elementwise_ops(backend, oracle_kernels):

@@ -80,6 +80,22 @@ def test_row_ops_reject_invalid(pkg):
     assert "leading dimension" in lib.hxmi_last_error().decode()
 
 
+def test_masked_softmax_validates_before_launch(pkg):
+    lib = pkg.load_library()
+    for fn in (lib.hxmi_softmax_masked_f16, lib.hxmi_softmax_masked_bf16):
+        # empty problems are no-ops (no pointer is touched)
+        assert fn(None, None, 0, 4, 4, 4, 16, 4, 16, None, 0, 0, 1, 0, 1.0, None) == 0
+        assert fn(None, None, 2, 4, 0, 4, 16, 4, 16, None, 0, 0, 1, 0, 1.0, None) == 0
+        assert fn(None, None, 2, 4, 4, 4, 16, 4, 16, None, 0, 0, 1, 0, 1.0, None) == 1  # null x / y
+        assert fn(16, 16, 2, 4, 8, 4, 16, 8, 32, None, 0, 0, 1, 0, 1.0, None) == 1  # ldx < s_kv
+        assert "row stride" in lib.hxmi_last_error().decode()
+        assert fn(16, 16, 2, 4, 4, 4, 8, 4, 16, None, 0, 0, 1, 0, 1.0, None) == 1  # slices overlap
+        assert fn(16, 16, 2, 4, 4, 4, 16, 4, 16, None, 0, 0, 1, 3, 1.0, None) == 1  # causal 3
+        assert "causal" in lib.hxmi_last_error().decode()
+        assert fn(16, 16, 2, 4, 4, 4, 16, 4, 16, 16, 4, 16, 0, 0, 1.0, None) == 1  # mask_group 0
+        assert fn(16, 16, 2, 4, 4, 4, 16, 4, 16, 17, 4, 16, 1, 0, 1.0, None) == 1  # odd mask address
+
+
 def test_w8a16_rejects_unaligned_k(pkg):
     lib = pkg.load_library()
     assert lib.hxmi_gemv_w8a16(16, 16, 16, None, 16, 1, 8, 24, 24, 32, 8, None, 0, None) == 1

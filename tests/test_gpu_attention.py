@@ -247,3 +247,118 @@ def test_attention_ex_rejects_bad_arguments(pkg, dev):
     assert rc == 1 and b"scale" in lib.hxmi_last_error()
     rc = lib.hxmi_attention_ex_f16(*args, 1, x.data_ptr(), 2, 0, 1, 0, 1.0, None)  # ldm below s_kv
     assert rc == 1 and b"mask row stride" in lib.hxmi_last_error()
+
+
+# ---- the three-step path with the mask operand (any head dim, bf16) ---------------------------------
+
+
+def _check_nan_tol(out, exp, rms):
+    """_check_nan with the RMS bound given: bf16 rounds S and P to 8 mantissa
+    bits against fp16's 11, so its RMS bar is 8x fp16's (the max-error bar
+    relative to the output's scale stays 1e-2)."""
+    o = np32(out)
+    nan_e = np.isnan(exp).all(-1)
+    assert np.array_equal(np.isnan(o).all(-1), nan_e) and not np.isnan(o[~nan_e]).any()
+    o, exp = o[~nan_e], exp[~nan_e]
+    assert ref.max_err_vs_scale(o, exp) <= TOL
+    assert np.sqrt(np.mean((o - exp) ** 2)) <= rms * np.sqrt(np.mean(exp**2)) + 1e-6
+
+
+RMS = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(
+    "b,h,s,skv,d,mshape",
+    [
+        (2, 3, 197, 197, 80, "b1"),  # head dim 80: not a fused-kernel shape
+        (1, 4, 77, 130, 32, "bh"),
+        (2, 2, 100, 256, 96, "ss"),
+        (1, 2, 33, 45, 64, "ss"),  # head dim 64: bf16 takes the three steps, fp16 the fused kernel
+    ],
+)
+def test_attention_three_step_masked(pkg, dev, dtype, b, h, s, skv, d, mshape):
+    q, k, v = (uniform(sh, 150 + i, dtype=dtype) for i, sh in enumerate([(b, h, s, d), (b, h, skv, d), (b, h, skv, d)]))
+    shape = {"b1": (b, 1, s, skv), "bh": (b, h, s, skv), "ss": (s, skv)}[mshape]
+    m = normal(shape, 154)
+    drop = torch.rand(shape, generator=torch.Generator().manual_seed(155)) < 0.2
+    m = m.masked_fill(drop, float("-inf"))
+    m[..., 0] = 0.0
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), d**-0.5, mask=m.cuda()).cpu()
+    assert out.dtype == dtype
+    _check_nan_tol(out, ref.sdpa(np32(q), np32(k), np32(v), d**-0.5, mask=np32(m)), RMS[dtype])
+
+
+@pytest.mark.parametrize(
+    "bh,s,skv,d,causal,dtype",
+    [
+        (4, 300, 300, 80, 1, torch.float16),
+        (3, 100, 300, 32, 2, torch.float16),  # bottom-right: queries are the last 100 positions
+        (2, 300, 100, 80, 2, torch.float16),  # S > S_kv: the first 200 queries see no key (NaN rows)
+        (2, 129, 129, 64, 1, torch.bfloat16),
+        (2, 64, 200, 128, 2, torch.bfloat16),
+    ],
+)
+def test_attention_three_step_causal(pkg, dev, bh, s, skv, d, causal, dtype):
+    q, k, v = uniform((bh, s, d), 171, dtype=dtype), uniform((bh, skv, d), 172, dtype=dtype), \
+        uniform((bh, skv, d), 173, dtype=dtype)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), 0.1, causal=causal).cpu()
+    _check_nan_tol(out, ref.sdpa(np32(q), np32(k), np32(v), 0.1, causal=causal), RMS[dtype])
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.float16, 80), (torch.bfloat16, 64), (torch.bfloat16, 128)])
+def test_attention_three_step_gqa_mask_causal(pkg, dev, dtype, d):
+    """Grouped K/V heads (8 query heads over 2) with a padding mask and the
+    causal rule: the query heads of one K/V head are one GEMM batch entry."""
+    b, hq, hkv, s = 2, 8, 2, 150
+    q, k, v = uniform((b, hq, s, d), 181, dtype=dtype), uniform((b, hkv, s, d), 182, dtype=dtype), \
+        uniform((b, hkv, s, d), 183, dtype=dtype)
+    m = torch.zeros((b, 1, s, s), dtype=torch.float16)
+    m[1, ..., 120:] = float("-inf")  # padded keys of the second batch row
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), mask=m.cuda(), causal=1).cpu()
+    exp = ref.sdpa(np32(q), np32(k), np32(v), d**-0.5, mask=np32(m), causal=1, kv_group=hq // hkv)
+    _check_nan_tol(out, exp, RMS[dtype])
+
+
+def test_attention_three_step_negative_scale(pkg, dev):
+    """scale <= 0 is outside the fused kernel's range: the three steps take it."""
+    q, k, v = uniform((3, 90, 64), 191), uniform((3, 70, 64), 192), uniform((3, 70, 64), 193)
+    out = pkg.attention(q.cuda(), k.cuda(), v.cuda(), -0.125, causal=2).cpu()
+    _check_nan_tol(out, ref.sdpa(np32(q), np32(k), np32(v), -0.125, causal=2), RMS[torch.float16])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_softmax_masked_through_abi(pkg, dev, dtype):
+    """hxmi_softmax_masked_*: scores [slices, s_q, s_kv] in padded rows, scale,
+    a mask shared by groups of two slices, causal = 2, in place and out of
+    place; every element against the oracle's masked softmax."""
+    lib = pkg.load_library()
+    fn = lib.hxmi_softmax_masked_f16 if dtype == torch.float16 else lib.hxmi_softmax_masked_bf16
+    slices, sq, skv, ld = 6, 37, 53, 56
+    x = normal((slices, sq, ld), 201, 3.0, dtype=dtype)
+    m = normal((3, sq, skv), 202)
+    m = m.masked_fill(torch.rand((3, sq, skv), generator=torch.Generator().manual_seed(203)) < 0.3, float("-inf"))
+    scale = 0.7
+    z = np32(x)[..., :skv] * np.float32(scale) + np.repeat(np32(m), 2, axis=0)
+    z = np.where(np.arange(skv)[None, :] > np.arange(sq)[:, None] + (skv - sq), np.float32(-np.inf), z)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(z - z.max(-1, keepdims=True))
+        want = e / e.sum(-1, keepdims=True)
+    xd, md = x.cuda(), m.cuda()
+    y = torch.full((slices, sq, skv), float("nan"), dtype=dtype, device=dev)
+    rc = fn(xd.data_ptr(), y.data_ptr(), slices, sq, skv, ld, sq * ld, skv, sq * skv, md.data_ptr(), skv, sq * skv,
+            2, 2, scale, None)
+    assert rc == 0, lib.hxmi_last_error()
+    rc = fn(xd.data_ptr(), xd.data_ptr(), slices, sq, skv, ld, sq * ld, ld, sq * ld, md.data_ptr(), skv, sq * skv,
+            2, 2, scale, None)
+    assert rc == 0, lib.hxmi_last_error()
+    torch.cuda.synchronize()
+    tol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    for got in (np32(y.cpu()), np32(xd.cpu())[..., :skv]):
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        ok = ~np.isnan(want)
+        assert np.abs(got[ok] - want[ok]).max() <= tol
+    # argument checks before any launch
+    assert fn(xd.data_ptr(), y.data_ptr(), slices, sq, skv, ld, sq * ld, skv, sq * skv, md.data_ptr(), skv, 0, 0, 1,
+              1.0, None) == 1  # mask_group 0
+    assert fn(xd.data_ptr(), y.data_ptr(), slices, sq, skv, ld, 1, skv, sq * skv, None, 0, 0, 1, 0, 1.0, None) == 1
