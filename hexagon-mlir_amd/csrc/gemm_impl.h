@@ -272,7 +272,7 @@ __device__ __forceinline__ void pp_barrier() {
 // loads its next step's fragments from LDS and issues the global->LDS loads,
 // so every SIMD's MFMA pipe alternates between its two waves.
 template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool NN, typename T, int EPI, bool OUTF32,
-          bool BI8 = false, bool PP = false, bool RMS = false, bool RAGGED = false, int SB = 0>
+          bool BI8 = false, bool PP = false, bool RMS = false, bool RAGGED = false, int SB = 0, int FD = 1>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a) {
   constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN, NT = NW * 64;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -579,8 +579,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
   }
   wait_vmcnt<(STAGES - 1) * NVM + WB>();
   __syncthreads();
-  short8v fa[2][TM], fb[2][TN];
-  read_frags(fa[0], fb[0], sa(0), sb(0), 0, 0);
+  // Fragments are read FD substeps ahead of their MFMAs: FD = 1 double
+  // buffers them; FD = 2 or 3 (64-deep K-steps) keeps one buffer per
+  // substep, so a read has FD substeps of MFMAs to return.  The K-step's
+  // wait and barrier come at the first substep that reads the next K-step
+  // (SUBS - FD): by then this wave has issued every read of the current
+  // step, and the barrier's wait for them lets the refill loads overwrite
+  // its stage.
+  static_assert(FD == 1 || (FD <= 3 && SUBS == 4 && !BI8), "fragment read distance");
+  constexpr int NFB = FD == 1 ? 2 : 4;
+  short8v fa[NFB][TM], fb[NFB][TN];
+  static_for<FD>([&](auto P) {
+    constexpr int p = decltype(P)::value;
+    read_frags(fa[p], fb[p], sa(0), sb(0), p, 0);
+  });
   int st = 0, stb = 0;
   for (int kt = 0; kt < nk; ++kt) {
     const int st1 = (st + 1 == STAGES) ? 0 : st + 1;
@@ -589,10 +601,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     const char* sB_ = sb(stb);
     static_for<SUBS>([&](auto S) {
       constexpr int s = decltype(S)::value;
-      constexpr int nxt = (s + 1) & 1;
-      if constexpr (s + 1 < SUBS) {
-        read_frags(fa[nxt], fb[nxt], sA_, sB_, s + 1, kt);
-      } else {
+      constexpr int t = s + FD;  // the substep whose fragments are read here
+      constexpr int cur = s % NFB, nxt = t % NFB;
+      if constexpr (t < SUBS) {
+        read_frags(fa[nxt], fb[nxt], sA_, sB_, t, kt);
+      } else if constexpr (t == SUBS) {
         wait_vmcnt<(STAGES - 2) * NVM + WB>();
         __syncthreads();
         // fragment reads first, then the refill loads: the same order as the
@@ -600,16 +613,18 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
         read_frags(fa[nxt], fb[nxt], sa(st1), sb(stb1), 0, kt + 1);
         issueA(kt + STAGES, st);
         issueB(kt + SBS, stb);
+      } else {
+        read_frags(fa[nxt], fb[nxt], sa(st1), sb(stb1), t - SUBS, kt + 1);
       }
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[s & 1][i], fa[s & 1][j], acc[i][j]);
+        for (int j = 0; j < TM; ++j) acc[i][j] = Mfma<T>::run(fb[cur][i], fa[cur][j], acc[i][j]);
       if constexpr (RMS) {
 #pragma unroll
-        for (int j = 0; j < TM; ++j) ss[j] = sumsq8<T>(fa[s & 1][j], ss[j]);
+        for (int j = 0; j < TM; ++j) ss[j] = sumsq8<T>(fa[cur][j], ss[j]);
       }
-      schedule_substep<TN * TM, NDS, (s + 1 < SUBS) ? 0 : NVM, RMS ? TM * 4 : 0>();
+      schedule_substep<TN * TM, NDS, (t == SUBS) ? NVM : 0, RMS ? TM * 4 : 0>();
       __builtin_amdgcn_sched_barrier(0);
     });
     st = st1;
@@ -853,6 +868,7 @@ struct TileShape {
   int BM, BN, WM, WN, BK, STAGES;
   bool PP = false;
   int SB = 0;  // B stages (0: as many as A)
+  int FD = 1;  // substeps between a fragment's LDS read and its MFMAs
 };
 
 // The small tiles run three LDS stages: their K-steps are short (a 64x64x64
@@ -861,6 +877,11 @@ struct TileShape {
 // flight while two or three workgroups still fit per CU.  Measured on the
 // TinyLlama block in sequence (weights not resident in L2): 91.0 -> 79.3 us;
 // four stages, at half the workgroups per CU, gave 87.1 us.
+// The tiles of at most 128 rows read their fragments three substeps ahead
+// (FD = 3): with one or two waves per SIMD and one to four MFMAs per wave
+// and substep, an LDS read issued one substep ahead had not returned by its
+// MFMA.  1024^3 NN on 64x64 tiles: 7.3 -> 6.3 us; the block's GEMMs and the
+// 256-row tiles (two waves per SIMD, eight MFMAs a substep) did not change.
 // The 384-row tiles (256x128 and 128x256, 48 KB per stage) hold one
 // workgroup per CU with two stages already, so a third costs no occupancy:
 // TinyLlama gate/up with SiLU-mul on the 8-wave 256x128 tile went 33.7 ->
@@ -868,19 +889,19 @@ struct TileShape {
 // four stages, one per CU, 40.8 / 42.0 us).
 constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 256, 128, 128, 64, 2},  // TILE_256x256
-    {128, 256, 64, 128, 64, 3},   // TILE_128x256
+    {128, 256, 64, 128, 64, 3, false, 0, 3},   // TILE_128x256
     {256, 128, 128, 64, 64, 3},   // TILE_256x128
-    {128, 128, 64, 64, 64, 2},    // TILE_128x128
-    {64, 128, 32, 64, 64, 3},     // TILE_64x128 (3 stages: see below)
-    {128, 64, 64, 32, 64, 3},     // TILE_128x64
-    {64, 64, 32, 32, 64, 3},      // TILE_64x64
+    {128, 128, 64, 64, 64, 2, false, 0, 3},    // TILE_128x128
+    {64, 128, 32, 64, 64, 3, false, 0, 3},     // TILE_64x128
+    {128, 64, 64, 32, 64, 3, false, 0, 3},     // TILE_128x64
+    {64, 64, 32, 32, 64, 3, false, 0, 3},      // TILE_64x64
     {256, 256, 128, 128, 32, 4},  // TILE_256x256_K32S4
     {256, 256, 128, 64, 64, 2},   // TILE_256x256_W8
     {128, 128, 64, 64, 32, 4},    // TILE_128x128_K32S4
     {256, 128, 128, 64, 32, 4},   // TILE_256x128_K32S4
     {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
     {256, 128, 64, 64, 64, 3},         // TILE_256x128_W8
-    {128, 128, 32, 64, 64, 2},         // TILE_128x128_W8
+    {128, 128, 32, 64, 64, 2, false, 0, 3},    // TILE_128x128_W8
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false, bool RAGGED = false>
@@ -894,7 +915,7 @@ hipError_t launch_one(const KArgs& k, hipStream_t stream) {
   constexpr int W8_A = s.BM * 128, W8_B = s.BN * 64;
   constexpr int W8_SB = W8_A / W8_B + 3 > 6 ? 6 : W8_A / W8_B + 3;
   hipLaunchKernelGGL((gemm_mfma<s.BM, s.BN, s.WM, s.WN, (BI8 ? 64 : s.BK), (BI8 ? 2 : s.STAGES), NN, T, EPI, OUTF32, BI8,
-                                (s.PP && !BI8 && !RMS), RMS, RAGGED, (BI8 ? W8_SB : s.SB)>),
+                                (s.PP && !BI8 && !RMS), RMS, RAGGED, (BI8 ? W8_SB : s.SB), (BI8 || s.PP ? 1 : s.FD)>),
                      dim3((unsigned)blocks), dim3(threads), 0, stream, k);
   return hipGetLastError();
 }
