@@ -149,6 +149,9 @@ int gemm_pick_tile(const GemmProblem& p) {
     // (the int8 896 -> 4864 projection at M = 256: 152 tiles of 128x64 run
     // 11.5 us against 13.4 us for 304 tiles of 64x64)
     if (i8 && c.id == TILE_128x64) eff = 0.62f;
+    // (the int8 lm_head 896 -> 151936 at M = 128: 1187 tiles of 128x128 at
+    // two per CU run 56.0 us against 72.0 us for 594 tiles of 128x256)
+    if (i8 && c.id == TILE_128x256) eff = 0.65f;
     const int64_t tm = (p.M + c.bm - 1) / c.bm, tn = (p.N + c.bn - 1) / c.bn;
     const int64_t tiles = tm * tn * p.batch;
     const int64_t slots = (int64_t)cus * c.per_cu;
