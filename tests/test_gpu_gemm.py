@@ -412,6 +412,18 @@ def test_gemm_split_k_default_down_projection(pkg, dev):
     assert ref.max_rel_err(np32(y), ref.linear(x.numpy(), w.numpy())) <= TOL
 
 
+@pytest.mark.parametrize("tile", TILES)
+def test_gemm_f32_out_every_tile(pkg, dev, force_tile, tile):
+    # fp32 output straight from the accumulators (HexKL's f16 x f16 -> f32
+    # matmul): integer operands, so every tile's result is exact
+    force_tile(tile)
+    g = torch.Generator().manual_seed(44)
+    act = torch.randint(-3, 4, (300, 200), generator=g).half()
+    w = torch.randint(-3, 4, (200, 264), generator=g).half()
+    out = pkg.hexkl_matmul(act.to(dev), w.to(dev)).cpu()
+    assert np.array_equal(out.numpy(), ref.matmul(act.numpy(), w.numpy()).astype(np.float32)), f"tile {tile}"
+
+
 def test_hexkl_compat_matmul(pkg, dev):
     # hexkl_linalg_matmul/wrapper.cpp:30-67: 1024x64 . 64x512, N(0,0.5)
     # rounded to 4 decimals, |diff| <= 1e-2 against a CPU triple loop
