@@ -546,10 +546,19 @@ __device__ __forceinline__ float4v tile_dot(const Shared& s, int sp, int rb, int
     }
     t += 8;
   }
-  for (; t < kfull; ++t) {
-    half8v av, bv;
-    ld(t, av, bv);
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc0, 0, 0, 0);
+  if (t < kfull) {
+    // the last (or only) 1..7 steps (a K-part of K = 896 over four waves
+    // is 7): every load first, then the MFMAs, so the steps wait out one
+    // LDS latency between them, not one each.  Slots past kfull reload the
+    // last step and feed no MFMA.
+    half8v av[8], bv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ld(min(t + i, kfull - 1), av[i], bv[i]);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      if (t + i < kfull) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[i], acc0, 0, 0, 0);
+      if (t + i + 1 < kfull) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i + 1], bv[i + 1], acc1, 0, 0, 0);
+    }
   }
   if (kfull < k1) {  // the last, partial step (np % 4 != 0)
     const int q = kfull * 4 + kq;
@@ -590,10 +599,17 @@ __device__ __forceinline__ float own_row(float4v acc, int c) {
   return c == 0 ? acc[0] : c == 1 ? acc[1] : c == 2 ? acc[2] : acc[3];
 }
 
-// Sum of the K-parts of tile row r in red[par] (parts 0..kp-1 at unit base..).
+// Sum of the K-parts of tile row r in red[par] (parts 0..kp-1 at unit base..),
+// in part order.  The reads go out together (a loop over the run-time part
+// count would wait out one LDS round trip per part).
 __device__ __forceinline__ float part_sum(const Shared& s, int par, int base, int kp, int r) {
+  float u[kNC];
+#pragma unroll
+  for (int p = 0; p < kNC; ++p) u[p] = s.red[par][base + min(p, kp - 1)][r];
   float v = 0.f;
-  for (int p = 0; p < kp; ++p) v += s.red[par][base + p][r];
+#pragma unroll
+  for (int p = 0; p < kNC; ++p)
+    if (p < kp) v += u[p];
   return v;
 }
 
@@ -671,13 +687,17 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
 
     // phase 0: RMSNorm, q|k|v projection (+bias); v is published
     {
+      // the biases of the first 16 rows, loaded before the poll (the finish
+      // of tile 0 adds lane m's to row m)
+      float bq = 0.f;
+      if (a.b_qkv && lane < min(16, g.rows0)) bq = (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + g.row00 + lane];
       weight_pieces(a.g_attn + (int64_t)l * rbH, kh, lane, gw);
       if (!poll_shared(a, XBc, l == 0 ? a.x : nullptr, H, tag, s.xin, w, s, nsync, gd)) return;
       norm_part(s, H, a.eps, kh, lane, gw);
       const bool ok = run_phase<false>(s, p0, 0, sl, sl + g.pre1, g.rows0, rbH, a.swzH, H, s.hin, w, lane, nsync, gd,
                                        [&](int m, float v, float) {
         const int row = g.row00 + m;
-        if (a.b_qkv) v += (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + row];
+        if (a.b_qkv) v += m < 16 ? bq : (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + row];
         const _Float16 y = (_Float16)v;
         if (a.qkv_out) ((_Float16*)a.qkv_out)[(int64_t)l * NQKV + row] = y;
         if (row >= H + NKV) publish(VB, a.strVB, row - H - NKV, tag << 16 | bits16(y));
