@@ -16,8 +16,12 @@
 //   * Loader waves stream the workgroup's rows of every layer's weights, in
 //     phase order, through a 128 KiB LDS ring with direct global->LDS loads,
 //     up to the ring's size ahead of the data dependencies.  A loader issues
-//     a batch of 16 KiB, waits for it, and publishes a batch count in LDS;
-//     kNL loaders interleave batches.
+//     a batch of 4 KiB, waits for it, and publishes a batch count in LDS;
+//     kNL = 4 loaders interleave batches, one loader and one compute wave
+//     per SIMD.  Small batches hand each phase its first rows sooner:
+//     loaders x KiB per batch measured 2 x 16: 535 us a forward (with the
+//     lm_head), 3 x 8: 528, 4 x 8: 524, 4 x 4: 521; 2 x 8: 591 (too little
+//     in flight) and 5 or more loaders 700+ (two loaders on a SIMD).
 //   * Compute waves take each phase's input vector from the workspace into
 //     LDS (one poller per workgroup), stage their K-part of the normalised
 //     (or expanded) input, and multiply 16-row tiles of the ring by it on
@@ -29,8 +33,8 @@
 //     with agent-scope stores into 8 copies.  Consumers load the words they
 //     need with agent-scope loads until every tag matches: a phase boundary
 //     costs one memory round trip (no grid barrier: arrive, release, read).
-// Measured on one MI355X (Qwen2.5-0.5B, 24 layers): ~520 us for the layers,
-// 4.6 us per phase.  A bare all-to-all chain of this kind (256 workgroups
+// Measured on one MI355X (Qwen2.5-0.5B, 24 layers): ~480 us for the layers,
+// 5.0 us per phase.  A bare all-to-all chain of this kind (256 workgroups
 // publish 4 words, every workgroup polls the 896) costs ~2 us per phase on
 // its own; streaming the weights at the same time slows the polls by
 // another ~0.7 us, and the MFMA work and its rendezvous are on the chain.
@@ -56,11 +60,11 @@ namespace hxmi {
 namespace {
 
 constexpr int kNC = 4;                   // compute waves per workgroup
-constexpr int kNL = 2;                   // loader waves per workgroup
+constexpr int kNL = 4;                   // loader waves per workgroup
 constexpr int kRing = 128 * 1024;        // LDS weight ring, bytes (power of two)
 constexpr int kChunk = 1024;             // one wave's direct-to-LDS load: 64 lanes x 16 B
 constexpr int kRingChunks = kRing / kChunk;
-constexpr int kBatch = 16;               // chunks per loader batch
+constexpr int kBatch = 4;                // chunks per loader batch
 constexpr int kPH = 4;                   // 8-element pieces per lane for K = hidden (<= 2048)
 constexpr int kPI = 12;                  // for K = intermediate (<= 6144)
 constexpr int kPoll = 8;                 // 16-byte poll groups per lane (vectors <= 8192)
