@@ -30,7 +30,7 @@
 //     phase.
 //   * Each phase output element is published as one 32-bit word, fp16 value
 //     in the low half and a 16-bit tag of (launch, layer) in the high half,
-//     with agent-scope stores into 8 copies.  Consumers load the words they
+//     with agent-scope stores into 2 copies.  Consumers load the words they
 //     need with agent-scope loads until every tag matches: a phase boundary
 //     costs one memory round trip (no grid barrier: arrive, release, read).
 // Measured on one MI355X (Qwen2.5-0.5B, 24 layers): ~480 us for the layers,
@@ -76,12 +76,11 @@ constexpr int kMaxTiles = 8;             // 16-row tiles of a phase run concurre
 constexpr int kTagBase = 0, kDone = 1, kAbort = 2, kError = DECODE_WS_ERROR_WORD, kCtrlWords = 64;
 constexpr uint32_t kSC1 = 16;  // buffer cache policy: agent-scope coherent
 // Each published vector is written in kCopies copies and workgroup b polls
-// copy b % kCopies (one per XCD when workgroups are dealt round-robin to the
-// XCDs): every polled line has 1/kCopies of the grid's pollers.  With all
-// 256 workgroups polling one copy, a phase boundary measured 2-3 us from the
-// last producer's store to the consumers' loads seeing it; one writer and
-// one poller see each other in 0.55 us.
-constexpr int kCopies = 8;
+// copy b % kCopies: every polled line has 1/kCopies of the grid's pollers.
+// Forwards with the lm_head measured 528 us with one copy, 514 with two,
+// 518 with four and 519 with eight (one writer and one poller see each
+// other in 0.55 us; more copies cost the producers more stores).
+constexpr int kCopies = 2;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -215,7 +215,7 @@ def test_noalloc_gemm_rejects_partials_beyond_its_scratch(pkg):
 def test_decode_step_rejects_before_launch(pkg):
     lib = pkg.load_library()
     need = lib.hxmi_decode_workspace_bytes(896, 128, 4864)
-    assert need == 4 * (64 + 8 * (2 * 896 + 128 + 4864))
+    assert need == 4 * (64 + 2 * (2 * 896 + 128 + 4864))  # control words + 2 copies of the vectors
     assert lib.hxmi_decode_workspace_bytes(0, 128, 4864) == 0
     P = 4096  # 256-byte aligned stand-in addresses: every call below fails before touching them
 
