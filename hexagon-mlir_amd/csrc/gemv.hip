@@ -357,7 +357,15 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
 // fp16 kernel keeps the plain order: its compiler schedule interleaves the
 // weight loads with the MFMAs in fewer registers, and the same restructure
 // measured slower there (lm_head M = 1 40.3 -> 42.1 us).
-template <int NWIN>
+// YS (M > 4): a workgroup's four waves take four consecutive tiles per
+// round; their y meets in LDS and leaves as 64-byte row pieces (16-byte
+// stores from one wave) instead of 4-byte stores from every lane.  At M = 16
+// the scattered stores cost ~3 us of the lm_head's 25 (a timing copy
+// without y stores ran 22.6 us); staged, paired runs on two boxes gained
+// 0.25-0.5 us (25.45 -> 24.98, 25.66 -> 25.42).  Rounds of eight
+// tiles (two per wave, 128-byte pieces) ran 27.8 us: twice the weight
+// streams in flight per wave, as with more workgroups.
+template <int NWIN, bool YS>
 __global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
   using T = _Float16;
   constexpr bool I8 = true;
@@ -418,41 +426,65 @@ __global__ __launch_bounds__(256) void gemv_pair_i8(VArgs a) {
   for (int i = 0; i < NXF; ++i) xs[(4 * i + w) * 64 + lane] = xr[i];
   __syncthreads();
 
-  for (bool first = true; tile < tiles; tile += stride, first = false) {
+  // YS: the same number of rounds for every wave (tiles past the end read
+  // zeros and store nothing); a round's first tile is tile - w.  Two LDS
+  // buffers, so one barrier a round suffices.
+  __shared__ __attribute__((aligned(16))) uint32_t ys[YS ? 2 : 1][16][16];
+  const int last = YS ? tiles + w : tiles;
+  int it = 0;
+  for (bool first = true; tile < last; tile += stride, first = false, ++it) {
     if (!first) fetch(tile);
-    float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    {
+      float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < NWIN; ++j) {
-      if (j < nwin) {
-        if constexpr (I8) {
+      for (int j = 0; j < NWIN; ++j) {
+        if (j < nwin) {
           const short8v lo = dequant8v((uint32_t)wv[j][0], (uint32_t)wv[j][1]);
           const short8v hi = dequant8v((uint32_t)wv[j][2], (uint32_t)wv[j][3]);
           acc0 = mfma16<T>(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 0) * 64 + lane]), acc0);
           acc0 = mfma16<T>(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 1) * 64 + lane]), acc0);
           acc1 = mfma16<T>(lo, __builtin_bit_cast(short8v, xs[(j * 4 + 2) * 64 + lane]), acc1);
           acc1 = mfma16<T>(hi, __builtin_bit_cast(short8v, xs[(j * 4 + 3) * 64 + lane]), acc1);
-        } else {
-          const short8v wf = __builtin_bit_cast(short8v, wv[j]);
-          acc0 = mfma16<T>(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 0) * 64 + lane]), acc0);
-          acc1 = mfma16<T>(wf, __builtin_bit_cast(short8v, xs[(j * 2 + 1) * 64 + lane]), acc1);
         }
       }
-    }
-    // D[r'][m]: lane holds m = lane % 16 and A rows r' = 4 (lane / 16) + i,
-    // i.e. halves 0, 1 of weight row n and of row n + 1
-    const int n = tile * 8 + 2 * kq;
-    const int m = lane & 15;
-    if (m < a.M) {
+      // D[r'][m]: lane holds m = lane % 16 and A rows r' = 4 (lane / 16) + i,
+      // i.e. halves 0, 1 of weight row n and of row n + 1
+      const int n = tile * 8 + 2 * kq;
+      const int m = lane & 15;
       const half2v s2 = __builtin_bit_cast(half2v, scb), b2 = __builtin_bit_cast(half2v, bib);
       const float sc0 = I8 ? (float)s2[0] : 1.f, sc1 = I8 ? (float)s2[1] : 1.f;
       const float v[2] = {(acc0[0] + acc1[1]) * sc0 + (float)b2[0], (acc0[2] + acc1[3]) * sc1 + (float)b2[1]};
-      T* yrow = (T*)(a.y + ((int64_t)m * a.ldy + n) * 2);
-      if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
-        T h2[2] = {(T)v[0], (T)v[1]};
-        *(uint32_t*)yrow = __builtin_bit_cast(uint32_t, h2);
-      } else {
-        if (n < a.N) yrow[0] = (T)v[0];
-        if (n + 1 < a.N) yrow[1] = (T)v[1];
+      T h2[2] = {(T)v[0], (T)v[1]};
+      const uint32_t bits = __builtin_bit_cast(uint32_t, h2);
+      if constexpr (YS) {
+        ys[it & 1][m][4 * w + kq] = bits;  // columns 8 w + 2 kq, + 1 of the round
+      } else if (m < a.M) {
+        T* yrow = (T*)(a.y + ((int64_t)m * a.ldy + n) * 2);
+        if (n + 1 < a.N && ((a.ldy | n) & 1) == 0) {
+          *(uint32_t*)yrow = bits;
+        } else {
+          if (n < a.N) yrow[0] = h2[0];
+          if (n + 1 < a.N) yrow[1] = h2[1];
+        }
+      }
+    }
+    if constexpr (YS) {
+      __syncthreads();
+      // wave 0 stores the round: lane l takes row l / 4, columns 8 (l % 4) .. + 7
+      if (w == 0) {
+        const int mr = lane >> 2, c = lane & 3;
+        const int n0 = tile * 8 + 8 * c;
+        if (mr < a.M && n0 < a.N) {
+          const int4v q = *(const int4v*)&ys[it & 1][mr][4 * c];
+          T* yrow = (T*)(a.y + ((int64_t)mr * a.ldy + n0) * 2);
+          if (n0 + 8 <= a.N && ((a.ldy | n0) & 7) == 0 && ((uintptr_t)a.y & 15) == 0) {
+            *(int4v*)yrow = q;
+          } else {
+            T e[8];
+            __builtin_memcpy(e, &q, 16);
+            for (int i = 0; i < 8 && n0 + i < a.N; ++i) yrow[i] = e[i];
+          }
+        }
       }
     }
   }
@@ -578,8 +610,12 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   int cap = I8 ? 512 : 1024;
   if (const int64_t e = knob(KNOB_GEMV_PAIR_WG); e != KNOB_UNSET && e > 0) cap = e < (1 << 20) ? (int)e : (1 << 20);
   if (blocks > cap) blocks = cap;
-  if constexpr (I8)
-    hipLaunchKernelGGL((gemv_pair_i8<8>), dim3(blocks), dim3(256), 0, stream, v);
+  if constexpr (I8) {
+    if (v.M > 4)
+      hipLaunchKernelGGL((gemv_pair_i8<8, true>), dim3(blocks), dim3(256), 0, stream, v);
+    else
+      hipLaunchKernelGGL((gemv_pair_i8<8, false>), dim3(blocks), dim3(256), 0, stream, v);
+  }
   else if (v.M > 4)
     hipLaunchKernelGGL((gemv_pair<T, false, 16, 16, 6>), dim3(blocks), dim3(256), 0, stream, v);
   else
