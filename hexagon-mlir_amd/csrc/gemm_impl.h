@@ -542,7 +542,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
 #pragma unroll
     for (int p = 0; p < D; ++p) issue(p, p);
     wait_vmcnt<(D - 1) * NVM>();
-    __syncthreads();
+    barrier_after_lds_loads();
     if (grp == 1) pp_barrier();
     short8v fa[SUBS][TM], fb[SUBS][TN];
     int st = 0, stw = D;
@@ -578,7 +578,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
     issueB(t + SBS, t + SBS);
   }
   wait_vmcnt<(STAGES - 1) * NVM + WB>();
-  __syncthreads();
+  barrier_after_lds_loads();  // (__syncthreads() would wait for every stage)
   // Fragments are read FD substeps ahead of their MFMAs: FD = 1 double
   // buffers them; FD = 2 or 3 (64-deep K-steps) keeps one buffer per
   // substep, so a read has FD substeps of MFMAs to return.  The K-step's
@@ -607,7 +607,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma(KArgs a)
         read_frags(fa[nxt], fb[nxt], sA_, sB_, t, kt);
       } else if constexpr (t == SUBS) {
         wait_vmcnt<(STAGES - 2) * NVM + WB>();
-        __syncthreads();
+        barrier_before_refill();
         // fragment reads first, then the refill loads: the same order as the
         // schedule below, so the loads can be spread between the MFMAs
         read_frags(fa[nxt], fb[nxt], sa(st1), sb(stb1), 0, kt + 1);

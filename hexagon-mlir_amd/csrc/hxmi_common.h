@@ -61,6 +61,30 @@ __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0f7
 
 __device__ __forceinline__ HXMI_LDS char* to_lds(char* p) { return (HXMI_LDS char*)(p); }
 
+// Workgroup barrier over LDS filled by direct-to-LDS loads, after the
+// caller's own partial wait for the loads it issued (wait_vmcnt<N>).
+// __syncthreads() opens with a release fence on LDS, before which the
+// compiler waits for every outstanding direct-to-LDS load (vmcnt(0)), the
+// prefetched later stages included; this barrier keeps the caller's wait.
+// It has the acquire half only (no LDS read moves above it), so it does not
+// publish ds_write data or retire earlier LDS reads: use it where the only
+// LDS data to share came in by direct loads and no stage is being refilled.
+__device__ __forceinline__ void barrier_after_lds_loads() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Barrier of a pipelined K-step, after the caller's wait for the stage read
+// next (wait_vmcnt<N>): every LDS read of this wave has returned
+// (lgkmcnt(0)), so refill loads issued after it overwrite no stage that a
+// wave still reads, and the later stages' loads stay in flight (they would
+// not under __syncthreads(), as above).
+__device__ __forceinline__ void barrier_before_refill() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt / expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group the 4x16 block of b16 values
 // addressed by the lanes (lane L supplies row L/4, columns 4*(L%4)..+3) is
 // returned transposed: lane i receives column i, rows 0..3.
