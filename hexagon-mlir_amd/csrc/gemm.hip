@@ -123,7 +123,7 @@ int gemm_pick_tile(const GemmProblem& p) {
   };
   // (the 8-wave 128x128 tile at two per CU outruns one 256x128 per CU on the
   // 512-token LLaMA MLP GEMMs; 64x64 at two per CU outruns 64x128 on the
-  // 512-token QKV projection, 416 vs 371 TFLOP/s; measured on the block shapes)
+  // 512-token O projection; measured on the block shapes)
   static const Cand cands[] = {
       {TILE_256x256_W8, 256, 256, 1, 1.00f}, {TILE_256x128_W8, 256, 128, 1, 0.85f},
       {TILE_128x256, 128, 256, 1, 0.80f},    {TILE_128x128_W8, 128, 128, 2, 0.90f},
@@ -152,6 +152,11 @@ int gemm_pick_tile(const GemmProblem& p) {
     // (the int8 lm_head 896 -> 151936 at M = 128: 1187 tiles of 128x128 at
     // two per CU run 56.0 us against 72.0 us for 594 tiles of 128x256)
     if (i8 && c.id == TILE_128x256) eff = 0.65f;
+    // an RMSNorm-folded GEMM sums the squares of its A rows in every tile of
+    // a row, so narrow tiles repeat that work more often (the 512-token QKV
+    // projection, 512x2560x2048, in the block sequence: 64x128 1.3 us faster
+    // than 64x64 once the K-step barriers kept the prefetch in flight)
+    if (p.rms && c.id == TILE_64x64) eff = 0.45f;
     const int64_t tm = (p.M + c.bm - 1) / c.bm, tn = (p.N + c.bn - 1) / c.bn;
     const int64_t tiles = tm * tn * p.batch;
     const int64_t slots = (int64_t)cus * c.per_cu;
@@ -274,7 +279,11 @@ static bool split_plan(const GemmProblem& p, GemmProblem& q, int& tile, int64_t&
   q.sA = kc;
   q.sB = p.b_nt ? kc : kc * p.ldb;
   q.sC = 0;
-  if (q.tile < 0 && gemm::knob_or(KNOB_GEMM_TILE, -1) < 0) q.tile = p.dtype == DT_W8A16 ? TILE_64x64 : TILE_64x128;
+  // (fp16: the two long slices of a down projection run 128x64 tiles, the
+  // 512x2048x5632 one 0.65 us faster in the block sequence than 64x128;
+  // ViT fc2's three slices of 1024 measured equal or slower with 128x64)
+  if (q.tile < 0 && gemm::knob_or(KNOB_GEMM_TILE, -1) < 0)
+    q.tile = p.dtype == DT_W8A16 ? TILE_64x64 : (splits == 2 && p.K / 2 >= 2048 ? TILE_128x64 : TILE_64x128);
   tile = gemm::tile_for(q);
   const gemm::TileShape s = gemm::kTiles[tile];
   const int64_t tiles = ((p.M + s.BM - 1) / s.BM) * ((p.N + s.BN - 1) / s.BN);
