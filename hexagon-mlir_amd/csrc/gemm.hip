@@ -157,6 +157,9 @@ int gemm_pick_tile(const GemmProblem& p) {
     // projection, 512x2560x2048, in the block sequence: 64x128 1.3 us faster
     // than 64x64 once the K-step barriers kept the prefetch in flight)
     if (p.rms && c.id == TILE_64x64) eff = 0.45f;
+    // long K with few tiles: 128x64 (4 waves, three per CU) over 64x64 and
+    // 64x128 (ViT-B/16 fc2, 1576x768x3072: 156 tiles)
+    if (!i8 && p.K >= 3072 && c.id == TILE_128x64) eff = 0.56f;
     const int64_t tm = (p.M + c.bm - 1) / c.bm, tn = (p.N + c.bn - 1) / c.bn;
     const int64_t tiles = tm * tn * p.batch;
     const int64_t slots = (int64_t)cus * c.per_cu;
@@ -232,9 +235,10 @@ hipError_t launch_fast(const GemmProblem& p, int tile, const KArgs& k, hipStream
 // problems run 64x128 tiles (4 waves, two per CU at three LDS stages).
 // Slices of >= 2048 of K that already give every CU a workgroup stop at
 // two; otherwise the slice count aims at ~480 workgroups, each slice keeping
-// >= 1024 of K (ViT-B/16 fc2, 1576x768x3072: 3 slices, 48.4 us per ViT
-// block against 52.7 with 2).  With K below 3072 (the 512-token QKV and O
-// projections) every split measured slower.
+// >= 1024 of K.  With K below 4096 every split measured slower: the
+// 512-token QKV and O projections, and ViT-B/16 fc2 (1576x768x3072) once
+// the K-step barriers kept the prefetch in flight (whole on 128x64 tiles
+// 0.9 us faster per ViT attention + MLP than 3 slices of 64x128).
 // With int8 weights the slices run 64x64 tiles (Qwen2.5-0.5B down
 // projection at M = 256: 105 -> 128 TFLOP/s).
 int gemm_splits(const GemmProblem& p) {
@@ -254,7 +258,7 @@ int gemm_splits(const GemmProblem& p) {
     return s;
   }
   const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 127) / 128);
-  if (tiles >= 384 || p.K < 3072) return 1;
+  if (tiles >= 384 || p.K < 4096) return 1;
   // long slices: two of them once every CU has a workgroup (measured in the
   // TinyLlama block sequence, weights not resident in L2: the 512x2048x5632
   // down projection ran 80.9 us per block with 2 slices, 83.0 with 3, 83.3

@@ -6,8 +6,7 @@ calls bench.py times (its own make_block / make_vit), against the oracle:
   epilogue over 2048 -> 11264, the O and down projections), stage by stage
   and end to end;
 * the ViT-B/16 MLP at batch 8 (fc1 1576x768 -> 3072 + bias + tanh-GELU, fc2
-  3072 -> 768 + bias, which splits K into the caller's workspace) and its
-  attention over 96 heads of 197 tokens.
+  3072 -> 768 + bias) and its attention over 96 heads of 197 tokens.
 
 Stage checks feed each kernel's own fp16 input to the oracle (elementwise
 max relative error <= 1e-2); the end-to-end checks chain the oracle's own
