@@ -134,3 +134,31 @@ def test_softmax_strided_rows(pkg, dev):
     got = np32(out.cpu())
     assert ref.max_rel_err(np32(y.cpu()), ref.softmax(base[:, :197].numpy(), 0.125)) <= TOL
     assert np.all(got[:, 197:] == 5.0)
+
+
+@pytest.mark.parametrize("rows,cols", [(5, 197), (7, 1), (3, 255), (9, 64), (4, 129), (1, 3)])
+def test_softmax_output_neighbours_untouched(pkg, dev, rows, cols):
+    # odd row counts (the last wave's second row group is past the matrix)
+    # and odd element counts: the output's neighbours in a larger buffer
+    # stay untouched
+    x = normal((rows, cols), 13)
+    buf = torch.full((rows * cols + 8,), 7.0, dtype=torch.float16, device=dev)
+    out = buf[:rows * cols].view(rows, cols)
+    y = pkg.softmax(x.to(dev), 0.3, out=out)
+    got = np32(buf.cpu())
+    assert ref.max_rel_err(np32(y.cpu()), ref.softmax(x.numpy(), 0.3)) <= TOL
+    assert np.all(got[rows * cols:] == 7.0)
+
+
+def test_softmax_unaligned_and_strided_rows_every_width(pkg, dev):
+    # rows starting 2 bytes past a 4-byte boundary, and padded rows, agree
+    # with the oracle at every width <= 256
+    for i, cols in enumerate([1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 197, 255, 256]):
+        rows = 3 + (i % 4)
+        flat = normal((rows * cols + 1,), 200 + i)
+        x = flat.to(dev)[1:].view(rows, cols)
+        y = pkg.softmax(x, 0.5)
+        assert ref.max_rel_err(np32(y.cpu()), ref.softmax(flat[1:].view(rows, cols).numpy(), 0.5)) <= TOL, cols
+        base = normal((rows, cols + 24), 300 + i)
+        ys = pkg.softmax(base.to(dev)[:, :cols], 0.5)
+        assert ref.max_rel_err(np32(ys.cpu()), ref.softmax(base[:, :cols].numpy(), 0.5)) <= TOL, cols
