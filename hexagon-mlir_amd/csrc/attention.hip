@@ -161,6 +161,16 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
 #pragma unroll
   for (int t = 0; t < DT; ++t) oacc[t] = float16v{};
   float m_run = -INFINITY, l_run = 0.f;
+  // This lane's V^T fragment reads for output tile dt sit at vbase[dt] plus
+  // a multiple of 4 rows: the chunk's V swizzle depends on (row & 3) only,
+  // so rows 4h + L/4 + 32b + 16t (+ 8) share one column offset.
+  int vbase[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const int g = lane >> 4, L = lane & 15;
+    const int d = dt * 32 + ((g & 1) << 4) + ((L & 3) << 2);
+    vbase[dt] = v_off<D>(4 * h + (L >> 2), d >> 3) + (d & 7) * 2;
+  }
 
   auto issue_chunk = [&](int c0) {
 #pragma unroll
@@ -223,21 +233,14 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
         }
       }
     };
-    // software pipeline: the MFMAs of the next block's scores (and its mask
-    // loads) run while this block's softmax occupies the vector ALUs
-    _Float16 mk_next[16];
-    if (MASK && kh < nblk) mask_vals(kh, mk_next);
-    float16v s_next = kh < nblk ? scores(kh) : float16v{};
-    for (int b = kh; b < nblk; b += KS) {
+    // Block b: its scores s (and mask entries mk) are in registers; the MFMAs
+    // of the next block's scores (and its mask loads) go out into s_nx / mk_nx
+    // first, so they run while this block's softmax occupies the vector
+    // ALUs.
+    auto block = [&](int b, float16v& s, float16v& s_nx, _Float16 (&mk)[16], _Float16 (&mk_nx)[16]) {
       const int kb = c0 + b * 32;
-      float16v s = s_next;
-      _Float16 mk[16];
-      if constexpr (MASK) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mk[i] = mk_next[i];
-        if (b + KS < nblk) mask_vals(b + KS, mk_next);
-      }
-      if (b + KS < nblk) s_next = scores(b + KS);
+      if (MASK && b + KS < nblk) mask_vals(b + KS, mk_nx);
+      if (b + KS < nblk) s_nx = scores(b + KS);
       // ragged keys and the causal rule only reach the blocks at their edges
       const bool edge = kb + 32 > a.skv || kb + 31 > q0 + a.causal_off;
       const bool scaled = MASK || edge;
@@ -282,23 +285,34 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) psum = __builtin_amdgcn_fdot2(p2[i], one2, psum, false);
       l_run += psum;
-      // two 16-key MFMA steps: step t uses keys {16t + 4h + j, 16t + 8 + 4h + j}
+      // two 16-key MFMA steps: step t uses keys {16t + 4h + j, 16t + 8 + 4h + j},
+      // at rows 32 b + 16 t (+ 8) past this lane's V base
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const short8v pf = __builtin_bit_cast(
             short8v, half8v{p2[4 * t][0], p2[4 * t][1], p2[4 * t + 1][0], p2[4 * t + 1][1], p2[4 * t + 2][0],
                             p2[4 * t + 2][1], p2[4 * t + 3][0], p2[4 * t + 3][1]});
-        const int g = lane >> 4, L = lane & 15;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const int d = dt * 32 + ((g & 1) << 4) + ((L & 3) << 2);
-          const int r1 = b * 32 + 16 * t + 4 * h + (L >> 2);
-          const short4v lo = lds_read_tr16(vs + v_off<D>(r1, d >> 3) + (d & 7) * 2);
-          const short4v hi = lds_read_tr16(vs + v_off<D>(r1 + 8, d >> 3) + (d & 7) * 2);
+          const char* vb = vs + vbase[dt] + (b * 32 + 16 * t) * RB;
+          const short4v lo = lds_read_tr16(vb);
+          const short4v hi = lds_read_tr16(vb + 8 * RB);
           const short8v vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           oacc[dt] = mfma32(vf, pf, oacc[dt]);
         }
       }
+    };
+    float16v s_next = kh < nblk ? scores(kh) : float16v{};
+    _Float16 mk_next[16];
+    if (MASK && kh < nblk) mask_vals(kh, mk_next);
+    for (int b = kh; b < nblk; b += KS) {
+      float16v s = s_next;
+      _Float16 mk[16];
+      if constexpr (MASK) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mk[i] = mk_next[i];
+      }
+      block(b, s, s_next, mk, mk_next);
     }
   }
 
