@@ -66,6 +66,20 @@ def test_w8a16_qwen_shapes(pkg, dev, M, K, N):
     assert ref.max_rel_err(np32(y.cpu()), ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy())) <= TOL
 
 
+@pytest.mark.parametrize("M,N", [(128, 151936), (200, 151936), (256, 133144)])
+def test_w8a16_many_tiles_with_bias(pkg, dev, M, N):
+    # one row of output tiles over more tiles than a round of workgroups,
+    # with a ragged last tile column and the bias epilogue
+    K = 896
+    x = normal((M, K), 500 + M)
+    q, s = int8_weights(N, K, 501)
+    b = normal((N,), 502)
+    y = pkg.w8a16_linear(x.to(dev), q.to(dev), s.to(dev), bias=b.to(dev))
+    torch.cuda.synchronize()
+    want = ref.w8a16_linear(x.numpy(), q.numpy(), s.numpy(), b.numpy())
+    assert ref.max_rel_err(np32(y.cpu()), want) <= TOL
+
+
 @pytest.fixture
 def gemv_path(knobs):
     """Force the decode kernel: "mfma" (16-row MFMA tiles, K split over
