@@ -20,6 +20,7 @@ fp32) on the same block, on the host's allowed threads and on one thread.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import gc
 import json
 import os
@@ -320,8 +321,11 @@ def bench_decode_full(pkg, torch, dev, timer, iters):
     the one key, o + residual, gate|up, SiLU-mul, down + residual, final norm,
     lm_head), 0.99 GB of fp16 weights: as the persistent decode kernel (one
     launch + the lm_head GEMV) and as the same step from separate library
-    launches (RMSNorm, GEMV, torch elementwise glue), both in HIP graphs.  The
-    two outputs are compared before anything is timed."""
+    launches (RMSNorm, GEMV, torch elementwise glue), both in HIP graphs; the
+    persistent kernel also with each layer's o projection folded onto the
+    normalised layer input (DecoderStack.fold_o: three dependent phases a
+    layer instead of four; the folding is weight preparation, done before
+    the timed region).  The outputs are compared before anything is timed."""
     H, KV, I, V, L, heads, kvh = 896, 128, 4864, 151936, 24, 14, 2
     g = torch.Generator(device=dev).manual_seed(11)
     rnd = lambda *s, std=0.02, mean=0.0: (torch.randn(*s, generator=g, device=dev) * std + mean).half()
@@ -345,17 +349,22 @@ def bench_decode_full(pkg, torch, dev, timer, iters):
             xs = xs + pkg.gemv(a, st.w_down[l])
         return pkg.gemv(pkg.rms_norm(xs, st.g_final, st.eps), st.w_lm)
 
+    stf = dataclasses.replace(st).fold_o()
     out = pkg.hxmi.decode_step(x, st)
+    outf = pkg.hxmi.decode_step(x, stf)
     ref_logits = chained()
     torch.cuda.synchronize()
     status = pkg.hxmi.decode_status()
     err = ((out["logits"].float() - ref_logits[0].float()).abs().max() / ref_logits.float().abs().max()).item()
-    if status != 0 or not err < 1e-2:
-        raise SystemExit(f"[bench] decode step check failed: status {status}, logits rel err {err}")
+    errf = ((outf["logits"].float() - ref_logits[0].float()).abs().max() / ref_logits.float().abs().max()).item()
+    if status != 0 or not err < 1e-2 or not errf < 1e-2:
+        raise SystemExit(f"[bench] decode step check failed: status {status}, logits rel err {err} / folded {errf}")
     nbytes = 2 * sum(t.numel() for t in (st.w_qkv, st.b_qkv, st.w_o, st.w_gu, st.w_down, st.g_attn, st.g_mlp,
                                          st.g_final, st.w_lm))
-    res = {"bytes": nbytes, "logits_rel_err_vs_chained": round(err, 5)}
-    for name, fn in (("persistent", lambda i: pkg.hxmi.decode_step(x, st)), ("chained_launches", chained)):
+    res = {"bytes": nbytes, "logits_rel_err_vs_chained": round(err, 5),
+           "folded_o_logits_rel_err_vs_chained": round(errf, 5)}
+    for name, fn in (("persistent", lambda i: pkg.hxmi.decode_step(x, st)),
+                     ("persistent_folded_o", lambda i: pkg.hxmi.decode_step(x, stf)), ("chained_launches", chained)):
         ms = timer.graph_ms(fn, iters)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 1), "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
@@ -365,7 +374,7 @@ def bench_decode_full(pkg, torch, dev, timer, iters):
     if status != 0:
         raise SystemExit(f"[bench] decode step: a wait expired during the timed graph replays (status {status})")
     res["status_after_replays"] = status
-    del st
+    del st, stf
     return res
 
 

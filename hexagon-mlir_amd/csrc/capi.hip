@@ -548,18 +548,20 @@ int64_t hxmi_decode_workspace_bytes(int64_t hidden, int64_t kv_dim, int64_t inte
   return hxmi::decode_workspace_bytes(hidden, kv_dim, intermediate);
 }
 
-int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_o, const void* w_gu,
-                         const void* w_down, const void* g_attn, const void* g_mlp, const void* g_final,
-                         const void* w_lm, void* qkv_out, void* x_out, void* h_out, void* logits, int64_t layers,
-                         int64_t hidden, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t intermediate,
-                         int64_t vocab, float eps, int64_t timeout_us, void* workspace, int64_t workspace_bytes,
-                         void* stream) {
-  const char* name = "hxmi_decode_step_f16";
+// The decode step with the o projection as w_o (w_ov null) or folded onto
+// the normalised input as w_ov, b_ov.
+static int decode_common(const char* name, const void* x, const void* w_qkv, const void* b_qkv, const void* w_o,
+                         const void* w_ov, const void* b_ov, const void* w_gu, const void* w_down, const void* g_attn,
+                         const void* g_mlp, const void* g_final, const void* w_lm, void* qkv_out, void* x_out,
+                         void* h_out, void* logits, int64_t layers, int64_t hidden, int64_t heads, int64_t kv_heads,
+                         int64_t head_dim, int64_t intermediate, int64_t vocab, float eps, int64_t timeout_us,
+                         void* workspace, int64_t workspace_bytes, void* stream) {
   REQUIRE(layers > 0 && hidden > 0 && heads > 0 && kv_heads > 0 && head_dim > 0 && intermediate > 0,
           "%s: sizes must be positive", name);
   REQUIRE(layers <= 4096, "%s: at most 4096 layers, got %lld", name, (long long)layers);
-  REQUIRE(x && w_qkv && w_o && w_gu && w_down && g_attn && g_mlp && g_final && h_out && workspace,
+  REQUIRE(x && w_qkv && (w_o || w_ov) && w_gu && w_down && g_attn && g_mlp && g_final && h_out && workspace,
           "%s: null pointer", name);
+  REQUIRE(!b_ov || al(b_ov, 2), "%s: b_ov must be 2-byte aligned", name);
   REQUIRE(!w_lm || (logits && vocab > 0), "%s: w_lm needs logits and vocab > 0", name);
   REQUIRE(eps >= 0.f, "%s: eps must be >= 0", name);
   const int64_t kv_dim = kv_heads * head_dim;
@@ -572,7 +574,7 @@ int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, co
                 "%s: unsupported shape (hidden %lld, heads %lld, kv_heads %lld, head_dim %lld, intermediate %lld)",
                 name, (long long)hidden, (long long)heads, (long long)kv_heads, (long long)head_dim,
                 (long long)intermediate);
-  for (const void* p : {x, w_qkv, w_o, w_gu, w_down, g_attn, g_mlp, g_final, (const void*)h_out})
+  for (const void* p : {x, w_qkv, w_o ? w_o : w_ov, w_gu, w_down, g_attn, g_mlp, g_final, (const void*)h_out})
     REQUIRE(al(p, 16), "%s: x, weights and outputs must be 16-byte aligned", name);
   REQUIRE(!x_out || al(x_out, 16), "%s: x_out must be 16-byte aligned", name);
   REQUIRE(!qkv_out || al(qkv_out, 2), "%s: qkv_out must be 2-byte aligned", name);
@@ -581,6 +583,8 @@ int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, co
   p.w_qkv = w_qkv;
   p.b_qkv = b_qkv;
   p.w_o = w_o;
+  p.w_ov = w_ov;
+  p.b_ov = b_ov;
   p.w_gu = w_gu;
   p.w_down = w_down;
   p.g_attn = g_attn;
@@ -603,6 +607,30 @@ int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, co
   if (!w_lm) return ok();
   return gemv_common(hxmi::DT_F16, name, h_out, w_lm, nullptr, logits, 1, vocab, hidden, hidden, hidden, vocab,
                      nullptr, 0, stream);
+}
+
+int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_o, const void* w_gu,
+                         const void* w_down, const void* g_attn, const void* g_mlp, const void* g_final,
+                         const void* w_lm, void* qkv_out, void* x_out, void* h_out, void* logits, int64_t layers,
+                         int64_t hidden, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t intermediate,
+                         int64_t vocab, float eps, int64_t timeout_us, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+  REQUIRE(w_o, "hxmi_decode_step_f16: null pointer");
+  return decode_common("hxmi_decode_step_f16", x, w_qkv, b_qkv, w_o, nullptr, nullptr, w_gu, w_down, g_attn, g_mlp,
+                       g_final, w_lm, qkv_out, x_out, h_out, logits, layers, hidden, heads, kv_heads, head_dim,
+                       intermediate, vocab, eps, timeout_us, workspace, workspace_bytes, stream);
+}
+
+int hxmi_decode_step_ov_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_ov, const void* b_ov,
+                            const void* w_gu, const void* w_down, const void* g_attn, const void* g_mlp,
+                            const void* g_final, const void* w_lm, void* qkv_out, void* x_out, void* h_out,
+                            void* logits, int64_t layers, int64_t hidden, int64_t heads, int64_t kv_heads,
+                            int64_t head_dim, int64_t intermediate, int64_t vocab, float eps, int64_t timeout_us,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  REQUIRE(w_ov, "hxmi_decode_step_ov_f16: null pointer");
+  return decode_common("hxmi_decode_step_ov_f16", x, w_qkv, b_qkv, nullptr, w_ov, b_ov, w_gu, w_down, g_attn, g_mlp,
+                       g_final, w_lm, qkv_out, x_out, h_out, logits, layers, hidden, heads, kv_heads, head_dim,
+                       intermediate, vocab, eps, timeout_us, workspace, workspace_bytes, stream);
 }
 
 int hxmi_decode_status(void* workspace, int clear, int* status, void* stream) {

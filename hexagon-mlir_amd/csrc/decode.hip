@@ -90,6 +90,8 @@ struct DArgs {
   const char* w_qkv;
   const char* b_qkv;
   const char* w_o;
+  const char* w_ov;  // o projection folded onto the normalised input (fold: w_o unused)
+  const char* b_ov;
   const char* w_gu;
   const char* w_down;
   const char* g_attn;
@@ -100,6 +102,7 @@ struct DArgs {
   char* h_out;
   uint32_t* ws;
   int L, H, NKV, I, HD, grp;
+  int fold;  // 1: the o rows run in phase 0 on w_ov (no phase 1)
   int offXB, offX1B, offVB, offAB;  // word offsets of the published vectors (copy 0)
   int strXB, strVB, strAB;         // words between copies
   int swzH, swzI;                  // ring piece swizzle masks for rows of H / I elements
@@ -124,10 +127,16 @@ struct Shared {
 };
 
 // Bytes of each phase of one layer in this workgroup's weight stream.  Phase
-// 0: q|k|v rows, 1: o rows, 2: gate/up rows (pairs x 2), 3: down rows.
+// 0: q|k|v rows, 1: o rows, 2: gate/up rows (pairs x 2), 3: down rows.  With
+// the o projection folded (fold), phase 0 streams the workgroup's o rows of
+// w_ov and then its q|k|v rows, and phase 1 is empty.  The o rows come first
+// so that they are all in tile 0: the finish of tile 0 runs on compute wave
+// 0, which also polls the next phase's input into s.xin, and the o rows'
+// residual reads x from s.xin (the host keeps a workgroup's o rows <= 16).
 // Named fields, not arrays: an array indexed by a run-time phase would live
 // in scratch memory.
 struct Geo {
+  int ro;                          // fold: o rows of this workgroup (the first rows of phase 0), else 0
   int rows0, rows1, rows2, rows3;  // rows in the stream (phase 2: 2 per pair)
   int row00, row01, row02, row03;  // first global row (phase 2: first pair)
   int bytes0, bytes1, bytes2, bytes3;
@@ -141,9 +150,10 @@ __device__ __forceinline__ Geo make_geo(const DArgs& a, int w, int G) {
   auto cnt = [&](int n) { return (int)((int64_t)n * (w + 1) / G) - lo(n); };
   Geo g;
   g.row00 = lo(a.H + 2 * a.NKV);
-  g.rows0 = cnt(a.H + 2 * a.NKV);
   g.row01 = lo(a.H);
-  g.rows1 = cnt(a.H);
+  g.ro = a.fold ? cnt(a.H) : 0;
+  g.rows0 = g.ro + cnt(a.H + 2 * a.NKV);
+  g.rows1 = a.fold ? 0 : cnt(a.H);
   g.row02 = lo(a.I);
   g.rows2 = 2 * cnt(a.I);
   g.row03 = lo(a.H);
@@ -220,8 +230,8 @@ struct Guard {
 // bytes apart, so unswizzled the 16 lanes would hit the same LDS banks.
 // swz + 1 divides the row's piece count.
 template <int P>
-__device__ __forceinline__ void issue_chunk(const DArgs& a, Shared& s, int row0, int bytes, int l, int off, int slot,
-                                            int lane) {
+__device__ __forceinline__ void issue_chunk(const DArgs& a, Shared& s, const Geo& g, int bytes, int l, int off,
+                                            int slot, int lane) {
   const int o = off + lane * 16;
   if (o >= bytes) return;
   const int rb = (P == 3 ? a.I : a.H) * 2;
@@ -231,18 +241,23 @@ __device__ __forceinline__ void issue_chunk(const DArgs& a, Shared& s, int row0,
   const char* base;
   int row;
   if constexpr (P == 0) {
-    base = a.w_qkv + (int64_t)l * (a.H + 2 * a.NKV) * rb;
-    row = row0 + m;
+    if (m < g.ro) {  // fold: the o rows of w_ov before the q|k|v rows
+      base = a.w_ov + (int64_t)l * a.H * rb;
+      row = g.row01 + m;
+    } else {
+      base = a.w_qkv + (int64_t)l * (a.H + 2 * a.NKV) * rb;
+      row = g.row00 + (m - g.ro);
+    }
   } else if constexpr (P == 1) {
     base = a.w_o + (int64_t)l * a.H * rb;
-    row = row0 + m;
+    row = g.row01 + m;
   } else if constexpr (P == 2) {
     // rows of the stream alternate gate row i, up row i of this workgroup's pairs
     base = a.w_gu + (int64_t)l * 2 * a.I * rb;
-    row = ((m & 1) ? a.I : 0) + row0 + (m >> 1);
+    row = ((m & 1) ? a.I : 0) + g.row02 + (m >> 1);
   } else {
     base = a.w_down + (int64_t)l * a.H * rb;
-    row = row0 + m;
+    row = g.row03 + m;
   }
   __builtin_amdgcn_global_load_lds((const void*)(base + (int64_t)row * rb + col),
                                    (HXMI_LDS void*)(s.ring + slot * kChunk), 16, 0, 0);
@@ -262,7 +277,6 @@ __device__ __forceinline__ void loader(const DArgs& a, Shared& s, const Geo& g, 
     for (int p = 0; p < 4; ++p) {
       const int pc = (p == 0 ? g.pre1 : p == 1 ? g.pre2 - g.pre1 : p == 2 ? g.pre3 - g.pre2 : g.pre4 - g.pre3) / kChunk;
       const int bytes = p == 0 ? g.bytes0 : p == 1 ? g.bytes1 : p == 2 ? g.bytes2 : g.bytes3;
-      const int row0 = p == 0 ? g.row00 : p == 1 ? g.row01 : p == 2 ? g.row02 : g.row03;
       for (int k = 0; k < pc; ++k, ++c) {
         const int b = c / kBatch;
         if (b % kNL != j) {  // another loader's batch: skip to its end (or the phase's)
@@ -284,10 +298,10 @@ __device__ __forceinline__ void loader(const DArgs& a, Shared& s, const Geo& g, 
           cfence();
         }
         const int off = k * kChunk, slot = c % kRingChunks;
-        if (p == 0) issue_chunk<0>(a, s, row0, bytes, l, off, slot, gd.lane);
-        else if (p == 1) issue_chunk<1>(a, s, row0, bytes, l, off, slot, gd.lane);
-        else if (p == 2) issue_chunk<2>(a, s, row0, bytes, l, off, slot, gd.lane);
-        else issue_chunk<3>(a, s, row0, bytes, l, off, slot, gd.lane);
+        if (p == 0) issue_chunk<0>(a, s, g, bytes, l, off, slot, gd.lane);
+        else if (p == 1) issue_chunk<1>(a, s, g, bytes, l, off, slot, gd.lane);
+        else if (p == 2) issue_chunk<2>(a, s, g, bytes, l, off, slot, gd.lane);
+        else issue_chunk<3>(a, s, g, bytes, l, off, slot, gd.lane);
         if (c % kBatch == kBatch - 1 || c == total - 1) {
           wait_vmcnt0();
           cfence();
@@ -684,36 +698,52 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
   const KPart kh = k_part(H, p0.kp, w), ki = k_part(I, p3.kp, w);
   u32x4 gw[kGP];
 
+  int ph = 0;  // phases run so far: consecutive phases use the two partial-sum sets in turn
   for (int l = 0; l < a.L; ++l) {
     const uint32_t tag = 1 + (base + l) % 65535u, tagn = 1 + (base + l + 1) % 65535u;
     const int sl = l * g.pre4;
 
-    // phase 0: RMSNorm, q|k|v projection (+bias); v is published
+    // phase 0: RMSNorm, q|k|v projection (+bias); v is published.  With the
+    // o projection folded, the o rows come first (x1 = x + h . w_ov^T +
+    // b_ov, published for phase 2) and v is not published
     {
       // the biases of the first 16 rows, loaded before the poll (the finish
       // of tile 0 adds lane m's to row m)
       float bq = 0.f;
-      if (a.b_qkv && lane < min(16, g.rows0)) bq = (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + g.row00 + lane];
+      if (lane < min(16, g.rows0)) {
+        if (lane < g.ro) {
+          if (a.b_ov) bq = (float)((const _Float16*)a.b_ov)[(int64_t)l * H + g.row01 + lane];
+        } else if (a.b_qkv) {
+          bq = (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + g.row00 + lane - g.ro];
+        }
+      }
       weight_pieces(a.g_attn + (int64_t)l * rbH, kh, lane, gw);
       if (!poll_shared(a, XBc, l == 0 ? a.x : nullptr, H, tag, s.xin, w, s, nsync, gd)) return;
       norm_part(s, H, a.eps, kh, lane, gw);
-      const bool ok = run_phase<false>(s, p0, 0, sl, sl + g.pre1, g.rows0, rbH, a.swzH, H, s.hin, w, lane, nsync, gd,
-                                       [&](int m, float v, float) {
-        const int row = g.row00 + m;
-        if (a.b_qkv) v += m < 16 ? bq : (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + row];
-        const _Float16 y = (_Float16)v;
-        if (a.qkv_out) ((_Float16*)a.qkv_out)[(int64_t)l * NQKV + row] = y;
-        if (row >= H + NKV) publish(VB, a.strVB, row - H - NKV, tag << 16 | bits16(y));
+      const bool ok = run_phase<false>(s, p0, ph++ & 1, sl, sl + g.pre1, g.rows0, rbH, a.swzH, H, s.hin, w, lane,
+                                       nsync, gd, [&](int m, float v, float) {
+        if (m < g.ro) {  // (tile 0: wave 0)
+          const int row = g.row01 + m;
+          if (a.b_ov) v += bq;
+          const _Float16 x1 = (_Float16)((float)s.xin[row] + (float)(_Float16)v);
+          publish(X1B, a.strXB, row, tag << 16 | bits16(x1));
+        } else {
+          const int row = g.row00 + (m - g.ro);
+          if (a.b_qkv) v += m < 16 ? bq : (float)((const _Float16*)a.b_qkv)[(int64_t)l * NQKV + row];
+          const _Float16 y = (_Float16)v;
+          if (a.qkv_out) ((_Float16*)a.qkv_out)[(int64_t)l * NQKV + row] = y;
+          if (!a.fold && row >= H + NKV) publish(VB, a.strVB, row - H - NKV, tag << 16 | bits16(y));
+        }
       });
       if (!ok) return;
     }
 
     // phase 1: o projection of the attention output, + residual
-    {
+    if (!a.fold) {
       if (!poll_shared(a, VBc, nullptr, NKV, tag, s.vin, w, s, nsync, gd)) return;
       attn_part(s, a.HD, a.grp, kh, lane);
-      const bool ok = run_phase<false>(s, p1, 1, sl + g.pre1, sl + g.pre2, g.rows1, rbH, a.swzH, H, s.hin, w, lane,
-                                       nsync, gd, [&](int m, float v, float) {
+      const bool ok = run_phase<false>(s, p1, ph++ & 1, sl + g.pre1, sl + g.pre2, g.rows1, rbH, a.swzH, H, s.hin, w,
+                                       lane, nsync, gd, [&](int m, float v, float) {
         const int row = g.row01 + m;
         const _Float16 x1 = (_Float16)((float)s.xin[row] + (float)(_Float16)v);
         publish(X1B, a.strXB, row, tag << 16 | bits16(x1));
@@ -726,8 +756,8 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
       weight_pieces(a.g_mlp + (int64_t)l * rbH, kh, lane, gw);
       if (!poll_shared(a, X1Bc, nullptr, H, tag, s.xin, w, s, nsync, gd)) return;
       norm_part(s, H, a.eps, kh, lane, gw);
-      const bool ok = run_phase<true>(s, p2, 0, sl + g.pre2, sl + g.pre3, g.rows2, rbH, a.swzH, H, s.hin, w, lane,
-                                      nsync, gd, [&](int i, float gv, float uv) {
+      const bool ok = run_phase<true>(s, p2, ph++ & 1, sl + g.pre2, sl + g.pre3, g.rows2, rbH, a.swzH, H, s.hin, w,
+                                      lane, nsync, gd, [&](int i, float gv, float uv) {
         const _Float16 gh = (_Float16)gv, uh = (_Float16)uv;
         const _Float16 sh = (_Float16)silu((float)gh);
         const _Float16 ah = (_Float16)((float)sh * (float)uh);
@@ -740,8 +770,8 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
     {
       // only this wave's K-part of the SiLU-mul output (pieces are 2 groups of 4 words)
       if (!poll_vector(a, ABc, I, 2 * ki.q0, 2 * ki.q1, tag, s.ain, gd)) return;
-      const bool ok = run_phase<false>(s, p3, 1, sl + g.pre3, sl + g.pre4, g.rows3, rbI, a.swzI, I, s.ain, w, lane,
-                                       nsync, gd, [&](int m, float v, float) {
+      const bool ok = run_phase<false>(s, p3, ph++ & 1, sl + g.pre3, sl + g.pre4, g.rows3, rbI, a.swzI, I, s.ain, w,
+                                       lane, nsync, gd, [&](int m, float v, float) {
         const int row = g.row03 + m;
         const _Float16 xn = (_Float16)((float)s.xin[row] + (float)(_Float16)v);
         publish(XB, a.strXB, row, tagn << 16 | bits16(xn));
@@ -808,12 +838,17 @@ bool decode_shape_ok(int64_t H, int64_t heads, int64_t kv_heads, int64_t head_di
 // at most one ring past the freed bytes: one 16-row tile (or the whole
 // phase, when a workgroup has fewer rows) must therefore fit the ring less
 // a batch and a chunk.  Row counts are the largest share of a workgroup
-// (ceil(rows / G)).  The stream offset of a layer is an int.
-static bool decode_grid_ok(int64_t H, int64_t kv, int64_t I, int64_t L, int64_t G) {
+// (ceil(rows / G)).  The stream offset of a layer is an int.  The rows whose
+// finish adds the residual from s.xin (o and down rows, H / G of them) must
+// fit one 16-row tile, which compute wave 0 finishes before it polls the
+// next phase's input into s.xin.
+static bool decode_grid_ok(int64_t H, int64_t kv, int64_t I, int64_t L, int64_t G, bool fold) {
   const int64_t room = kRing - (int64_t)(kBatch + 1) * kChunk;
   auto share = [&](int64_t n) { return (n + G - 1) / G; };
   auto tile_fits = [&](int64_t rows, int64_t K) { return std::min<int64_t>(rows, 16) * K * 2 <= room; };
-  const int64_t r0 = share(H + 2 * kv), r1 = share(H), r2 = 2 * share(I), r3 = share(H);
+  if (share(H) > 16) return false;
+  const int64_t r0 = share(H + 2 * kv) + (fold ? share(H) : 0), r1 = fold ? 0 : share(H), r2 = 2 * share(I),
+                r3 = share(H);
   if (!tile_fits(r0, H) || !tile_fits(r1, H) || !tile_fits(r2, H) || !tile_fits(r3, I)) return false;
   auto pad = [](int64_t b) { return (b + kChunk - 1) / kChunk * kChunk; };
   const int64_t layer = pad(r0 * H * 2) + pad(r1 * H * 2) + pad(r2 * H * 2) + pad(r3 * I * 2);
@@ -842,13 +877,16 @@ hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream) {
   // the vector it would overwrite (a published vector is rewritten one
   // layer later, after a phase that waited for that poller's own rows).
   const int G = (int)std::min<int64_t>(cus, std::min(p.H, p.I));
-  if (!decode_grid_ok(p.H, p.kv_heads * p.head_dim, p.I, p.L, G)) return hipErrorNotSupported;
+  if (!decode_grid_ok(p.H, p.kv_heads * p.head_dim, p.I, p.L, G, p.w_ov != nullptr)) return hipErrorNotSupported;
 
   DArgs a{};
   a.x = (const char*)p.x;
   a.w_qkv = (const char*)p.w_qkv;
   a.b_qkv = (const char*)p.b_qkv;
   a.w_o = (const char*)p.w_o;
+  a.w_ov = (const char*)p.w_ov;
+  a.b_ov = (const char*)p.b_ov;
+  a.fold = p.w_ov != nullptr;
   a.w_gu = (const char*)p.w_gu;
   a.w_down = (const char*)p.w_down;
   a.g_attn = (const char*)p.g_attn;

@@ -192,7 +192,9 @@ struct DecodeProblem {
   const void* x;        // [H] fp16: the token's embedding row
   const void* w_qkv;    // [L, H + 2*kv_dim, H]: q rows, k rows, v rows
   const void* b_qkv;    // [L, H + 2*kv_dim] or null
-  const void* w_o;      // [L, H, H]
+  const void* w_o;      // [L, H, H] (unused with w_ov)
+  const void* w_ov;     // [L, H, H] o projection folded onto the normalised input, or null
+  const void* b_ov;     // [L, H] its bias, or null
   const void* w_gu;     // [L, 2*I, H]: gate rows, then up rows
   const void* w_down;   // [L, H, I]
   const void* g_attn;   // [L, H] RMSNorm weights before attention

@@ -61,6 +61,7 @@ SIGNATURES = {
     "hxmi_fold_rmsnorm_weight_bf16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_quantize_int8_rows_f16": ([_P, _P, _P, _I64, _I64, _I64, _I64, _P], _I),
     "hxmi_decode_step_f16": ([_P] * 14 + [_I64] * 7 + [_F, _I64, _P, _I64, _P], _I),
+    "hxmi_decode_step_ov_f16": ([_P] * 15 + [_I64] * 7 + [_F, _I64, _P, _I64, _P], _I),
     "hxmi_decode_workspace_bytes": ([_I64, _I64, _I64], _I64),
     "hxmi_decode_status": ([_P, _I, ctypes.POINTER(_I), _P], _I),
     "hxmi_lwp_record": ([_P, _I64, ctypes.c_uint32, _P], _I),
@@ -676,7 +677,9 @@ class DecoderStack:
     w_qkv [L, H + 2*kv_dim, H] (q rows, k rows, v rows), b_qkv [L, H + 2*kv_dim]
     or None, w_o [L, H, H], w_gu [L, 2*I, H] (gate rows, then up rows), w_down
     [L, H, I], g_attn and g_mlp [L, H] (RMSNorm weights), g_final [H], w_lm
-    [vocab, H] or None (no logits)."""
+    [vocab, H] or None (no logits).  w_ov [L, H, H] and b_ov [L, H] (None
+    without b_qkv): the o projection folded onto the normalised layer input,
+    set by fold_o(); decode_step then runs three dependent phases a layer."""
     w_qkv: torch.Tensor
     b_qkv: Optional[torch.Tensor]
     w_o: torch.Tensor
@@ -689,12 +692,37 @@ class DecoderStack:
     kv_heads: int
     eps: float
     w_lm: Optional[torch.Tensor] = None
+    w_ov: Optional[torch.Tensor] = None
+    b_ov: Optional[torch.Tensor] = None
 
     @property
     def dims(self) -> tuple[int, int, int, int]:
         """(layers, hidden, intermediate, kv_dim)"""
         L, nqkv, H = self.w_qkv.shape
         return L, H, self.w_gu.shape[1] // 2, (nqkv - H) // 2
+
+    def fold_o(self) -> "DecoderStack":
+        """Sets w_ov = w_o E w_v and b_ov = w_o E b_v per layer, E copying key /
+        value head j's head_dim rows to every query head of its group: at
+        position 0 the attention output is E (h . w_v^T + b_v), so the o
+        projection becomes h . w_ov^T + b_ov on the layer's normalised input
+        h.  Computed with this library's NN GEMM and GEMV (fp32 accumulation,
+        one fp16 rounding).  Returns self."""
+        L, H, _, kv_dim = self.dims
+        hd = H // self.heads
+        grp = self.heads // self.kv_heads
+        i = torch.arange(H, device=self.w_qkv.device)
+        vrow = H + kv_dim + (i // hd // grp) * hd + i % hd  # the v row each o input element reads
+        w_ov = torch.empty((L, H, H), dtype=torch.float16, device=self.w_qkv.device)
+        b_ov = None if self.b_qkv is None else torch.empty((L, H), dtype=torch.float16, device=self.w_qkv.device)
+        for layer in range(L):
+            ev = self.w_qkv[layer].index_select(0, vrow).contiguous()
+            gemm(self.w_o[layer], ev, b_layout="nn", out=w_ov[layer])
+            if b_ov is not None:
+                eb = self.b_qkv[layer].index_select(0, vrow).reshape(1, H).contiguous()
+                gemv(eb, self.w_o[layer], out=b_ov[layer].view(1, H))
+        self.w_ov, self.b_ov = w_ov, b_ov
+        return self
 
 
 _DECODE_WS: "collections.OrderedDict[tuple, torch.Tensor]" = collections.OrderedDict()
@@ -733,7 +761,7 @@ def decode_step(x: torch.Tensor, stack: DecoderStack, *, out_qkv: bool = False,
     early; decode_status() reports it."""
     L, H, inter, kv_dim = stack.dims
     ts = [x, stack.w_qkv, stack.b_qkv, stack.w_o, stack.w_gu, stack.w_down, stack.g_attn, stack.g_mlp,
-          stack.g_final, stack.w_lm]
+          stack.g_final, stack.w_lm, stack.w_ov, stack.b_ov]
     _require_gpu(*ts)
     for t in ts:
         if t is not None and (t.dtype != torch.float16 or not t.is_contiguous()):
@@ -746,6 +774,11 @@ def decode_step(x: torch.Tensor, stack: DecoderStack, *, out_qkv: bool = False,
             raise HxmiError(f"{name} is {tuple(getattr(stack, name).shape)}, expected {shape}")
     if stack.b_qkv is not None and tuple(stack.b_qkv.shape) != (L, H + 2 * kv_dim):
         raise HxmiError("b_qkv must be [L, H + 2*kv_dim]")
+    if stack.w_ov is not None and tuple(stack.w_ov.shape) != (L, H, H):
+        raise HxmiError("w_ov must be [L, H, H]")
+    if (stack.b_ov is not None) != (stack.w_ov is not None and stack.b_qkv is not None) or (
+            stack.b_ov is not None and tuple(stack.b_ov.shape) != (L, H)):
+        raise HxmiError("b_ov must be [L, H] with w_ov and b_qkv, else None")
     if x.numel() != H:
         raise HxmiError(f"x has {x.numel()} elements, expected {H}")
     if stack.kv_heads * head_dim != kv_dim or stack.heads * head_dim != H:
@@ -761,11 +794,16 @@ def decode_step(x: torch.Tensor, stack: DecoderStack, *, out_qkv: bool = False,
     lib = load_library()
     nbytes = lib.hxmi_decode_workspace_bytes(H, kv_dim, inter)
     ws = _decode_workspace(dev, (H, kv_dim, inter), nbytes)
-    _check(lib.hxmi_decode_step_f16(
-        x.data_ptr(), stack.w_qkv.data_ptr(), _ptr(stack.b_qkv), stack.w_o.data_ptr(), stack.w_gu.data_ptr(),
-        stack.w_down.data_ptr(), stack.g_attn.data_ptr(), stack.g_mlp.data_ptr(), stack.g_final.data_ptr(),
-        _ptr(stack.w_lm), _ptr(qkv), xo.data_ptr(), h.data_ptr(), _ptr(logits), L, H, stack.heads, stack.kv_heads,
-        head_dim, inter, vocab, float(stack.eps), int(timeout_us), ws.data_ptr(), ws.numel() * 4, _stream(x)))
+    tail = (stack.w_gu.data_ptr(), stack.w_down.data_ptr(), stack.g_attn.data_ptr(), stack.g_mlp.data_ptr(),
+            stack.g_final.data_ptr(), _ptr(stack.w_lm), _ptr(qkv), xo.data_ptr(), h.data_ptr(), _ptr(logits), L, H,
+            stack.heads, stack.kv_heads, head_dim, inter, vocab, float(stack.eps), int(timeout_us), ws.data_ptr(),
+            ws.numel() * 4, _stream(x))
+    if stack.w_ov is not None:
+        _check(lib.hxmi_decode_step_ov_f16(x.data_ptr(), stack.w_qkv.data_ptr(), _ptr(stack.b_qkv),
+                                           stack.w_ov.data_ptr(), _ptr(stack.b_ov), *tail))
+    else:
+        _check(lib.hxmi_decode_step_f16(x.data_ptr(), stack.w_qkv.data_ptr(), _ptr(stack.b_qkv),
+                                        stack.w_o.data_ptr(), *tail))
     return {"h": h, "x": xo, "logits": logits, "qkv": qkv}
 
 

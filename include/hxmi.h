@@ -394,6 +394,33 @@ int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, co
                          int64_t vocab, float eps, int64_t timeout_us, void* workspace, int64_t workspace_bytes,
                          void* stream);
 
+/*
+ * hxmi_decode_step_f16 with each layer's o projection folded onto the
+ * normalised input h of the same layer: at position 0 the attention output
+ * is att = E (h . w_v^T + b_v) (E copies key/value head j's head_dim
+ * elements to every query head of its group), so
+ *   att . w_o^T = h . w_ov^T + b_ov,  w_ov = w_o E w_v,  b_ov = w_o E b_v
+ * (w_v, b_v: the v rows of w_qkv, b_qkv).  The step then runs the o
+ * projection with q|k|v from the same input and has three dependent phases
+ * a layer instead of four.  w_ov [L, H, H]; b_ov [L, H] or NULL (b_qkv
+ * NULL).  Per layer, with Ev = E w_v ([H, H], row i = v row (i / head_dim /
+ * (heads / kv_heads)) * head_dim + i % head_dim) and Eb = E b_v:
+ * w_ov = hxmi_gemm_f16 NN of w_o and Ev, b_ov = hxmi_gemv_f16 of Eb and
+ * w_o (fp32 accumulation, one fp16 rounding).  Everything else, the
+ * outputs and the workspace are as for hxmi_decode_step_f16; x1 differs
+ * from that step's by the rounding of w_ov and of the un-rounded v (fp16
+ * v is never formed).
+ * No counterpart in the reference: it serves the same one-token forward
+ * (benchmark_models/run_qwen2.5-0.5b.py:171-173, 224-233), for callers that
+ * keep the folded weights beside the stack.
+ */
+int hxmi_decode_step_ov_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_ov, const void* b_ov,
+                            const void* w_gu, const void* w_down, const void* g_attn, const void* g_mlp,
+                            const void* g_final, const void* w_lm, void* qkv_out, void* x_out, void* h_out,
+                            void* logits, int64_t layers, int64_t hidden, int64_t heads, int64_t kv_heads,
+                            int64_t head_dim, int64_t intermediate, int64_t vocab, float eps, int64_t timeout_us,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes of hxmi_decode_step_f16 for these sizes. */
 int64_t hxmi_decode_workspace_bytes(int64_t hidden, int64_t kv_dim, int64_t intermediate);
 

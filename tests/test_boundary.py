@@ -236,3 +236,13 @@ def test_decode_step_rejects_before_launch(pkg):
     assert call(hidden=4096, heads=64, ws_bytes=1 << 20) == 2
     assert call(inter=8192, ws_bytes=1 << 20) == 2
     assert "unsupported shape" in lib.hxmi_last_error().decode()
+
+    # the folded-o entry point checks the same way, and needs w_ov
+    def call_ov(w_ov=P, b_ov=None, layers=24, ptr=P):
+        return lib.hxmi_decode_step_ov_f16(ptr, P, None, w_ov, b_ov, P, P, P, P, P, None, None, None, P, None,
+                                           layers, 896, 14, 2, 64, 4864, 0, 1e-6, 0, P, need, None)
+
+    assert call_ov(w_ov=None) == 1 and "null" in lib.hxmi_last_error().decode()
+    assert call_ov(layers=0) == 1 and "positive" in lib.hxmi_last_error().decode()
+    assert call_ov(b_ov=P + 1) == 1 and "b_ov" in lib.hxmi_last_error().decode()
+    assert call_ov(w_ov=P + 2) == 1 and "16-byte" in lib.hxmi_last_error().decode()

@@ -1,4 +1,6 @@
-"""Persistent one-token decode step (hxmi_decode_step_f16) against the oracle.
+"""Persistent one-token decode step (hxmi_decode_step_f16, and
+hxmi_decode_step_ov_f16 with the o projection folded onto the normalised
+layer input, fold=True) against the oracle.
 
 The oracle (oracle.decode_step, pinned against transformers' Qwen2 forward in
 tests/test_decode_oracle.py) runs on the CPU from the same fp16 weights.  The
@@ -39,6 +41,18 @@ def make_stack(pkg, dev, layers, hidden, heads, kv_heads, inter, vocab, bias, ep
     return st, x, np_w
 
 
+@pytest.fixture(params=[False, True], ids=["o", "folded_o"])
+def fold(request):
+    return request.param
+
+
+def stack_for(pkg, dev, fold, **kw):
+    st, x, np_w = make_stack(pkg, dev, **kw)
+    if fold:
+        st.fold_o()
+    return st, x, np_w
+
+
 def oracle(x, st, np_w, fp16=True):
     return ref.decode_step(x.cpu().numpy(), heads=st.heads, kv_heads=st.kv_heads, eps=st.eps, fp16=fp16, **np_w)
 
@@ -59,16 +73,16 @@ def check(out, want, want32, tag, tol16=4e-3, tol32=1e-2):
     assert all(v < tol32 for v in errs32.values()), errs32
 
 
-def test_decode_step_qwen05b_matches_oracle(pkg, dev):
-    st, x, np_w = make_stack(pkg, dev, **QWEN, seed=1)
+def test_decode_step_qwen05b_matches_oracle(pkg, dev, fold):
+    st, x, np_w = stack_for(pkg, dev, fold, **QWEN, seed=1)
     out = pkg.hxmi.decode_step(x, st, out_qkv=True)
     torch.cuda.synchronize()
     assert pkg.hxmi.decode_status() == 0
     check(out, oracle(x, st, np_w), oracle(x, st, np_w, fp16=False), "qwen2.5-0.5b")
 
 
-def test_decode_step_tinyllama_dims(pkg, dev):
-    st, x, np_w = make_stack(pkg, dev, **TINYLLAMA, seed=2)
+def test_decode_step_tinyllama_dims(pkg, dev, fold):
+    st, x, np_w = stack_for(pkg, dev, fold, **TINYLLAMA, seed=2)
     out = pkg.hxmi.decode_step(x, st, out_qkv=True)
     torch.cuda.synchronize()
     assert pkg.hxmi.decode_status() == 0
@@ -79,17 +93,17 @@ def test_decode_step_tinyllama_dims(pkg, dev):
     dict(layers=2, hidden=64, heads=2, kv_heads=1, inter=40, vocab=96, bias=True, eps=1e-6),  # most CUs own no row
     dict(layers=5, hidden=520, heads=13, kv_heads=1, inter=1000, vocab=0, bias=False, eps=1e-6),  # ragged rows, 13 q heads per kv head
 ])
-def test_decode_step_small_and_ragged(pkg, dev, dims):
-    st, x, np_w = make_stack(pkg, dev, **dims, seed=3)
+def test_decode_step_small_and_ragged(pkg, dev, fold, dims):
+    st, x, np_w = stack_for(pkg, dev, fold, **dims, seed=3)
     out = pkg.hxmi.decode_step(x, st, out_qkv=True)
     torch.cuda.synchronize()
     assert pkg.hxmi.decode_status() == 0
     check(out, oracle(x, st, np_w), oracle(x, st, np_w, fp16=False), f"H{dims['hidden']}")
 
 
-def test_decode_step_repeats_exactly_with_fresh_inputs(pkg, dev):
+def test_decode_step_repeats_exactly_with_fresh_inputs(pkg, dev, fold):
     # every launch publishes under new tags: a launch never reads the previous one's vectors
-    st, x, np_w = make_stack(pkg, dev, layers=4, hidden=896, heads=14, kv_heads=2, inter=4864, vocab=0, bias=True,
+    st, x, np_w = stack_for(pkg, dev, fold, layers=4, hidden=896, heads=14, kv_heads=2, inter=4864, vocab=0, bias=True,
                              eps=1e-6, seed=4)
     x2 = torch.randn(896, generator=torch.Generator(device=dev).manual_seed(9), device=dev).half()
     a = pkg.hxmi.decode_step(x, st)
@@ -102,10 +116,10 @@ def test_decode_step_repeats_exactly_with_fresh_inputs(pkg, dev):
     assert not torch.equal(a["h"], b["h"])
 
 
-def test_decode_step_expired_wait_is_reported_and_recovered(pkg, dev):
+def test_decode_step_expired_wait_is_reported_and_recovered(pkg, dev, fold):
     # a 1 us bound on every wait: the launch gives up early (every wave still
     # leaves), the error word says so, and the next launch is correct
-    st, x, np_w = make_stack(pkg, dev, layers=4, hidden=896, heads=14, kv_heads=2, inter=4864, vocab=0, bias=True,
+    st, x, np_w = stack_for(pkg, dev, fold, layers=4, hidden=896, heads=14, kv_heads=2, inter=4864, vocab=0, bias=True,
                              eps=1e-6, seed=5)
     pkg.hxmi.decode_step(x, st, timeout_us=1)
     torch.cuda.synchronize()
@@ -139,3 +153,25 @@ def test_decode_step_is_the_chain_of_library_ops(pkg, dev):
     torch.cuda.synchronize()
     assert rel(out["h"].float().cpu().numpy(), h[0].float().cpu().numpy()) < 4e-3
     assert rel(out["logits"].float().cpu().numpy(), logits[0].float().cpu().numpy()) < 1e-2
+
+
+def test_fold_o_weights(pkg, dev):
+    """w_ov = w_o E w_v and b_ov = w_o E b_v per layer (E copies key/value head
+    j to the query heads of its group), against float64 on the CPU."""
+    st, x, np_w = make_stack(pkg, dev, layers=2, hidden=896, heads=14, kv_heads=2, inter=64, vocab=0, bias=True,
+                             eps=1e-6, seed=7)
+    st.fold_o()
+    H, kv, hd, grp = 896, 128, 64, 7
+    i = np.arange(H)
+    vrow = H + kv + (i // hd // grp) * hd + i % hd
+    for l in range(2):
+        wv = np_w["w_qkv"][l].astype(np.float64)[vrow]
+        want = np_w["w_o"][l].astype(np.float64) @ wv
+        got = st.w_ov[l].float().cpu().numpy()
+        assert ref.max_rel_err(got, want) <= 1e-2
+        wantb = np_w["w_o"][l].astype(np.float64) @ np_w["b_qkv"][l].astype(np.float64)[vrow]
+        assert ref.max_rel_err(st.b_ov[l].float().cpu().numpy(), wantb) <= 1e-2
+    # without biases there is no b_ov
+    st2, _, _ = make_stack(pkg, dev, layers=1, hidden=64, heads=2, kv_heads=1, inter=40, vocab=0, bias=False,
+                           eps=1e-6, seed=8)
+    assert st2.fold_o().b_ov is None
