@@ -792,7 +792,11 @@ __device__ __forceinline__ void compute(const DArgs& a, Shared& s, const Geo& g,
   }
 }
 
+// FOLD: the o projection folded into phase 0 (a.fold), as a compile-time
+// constant in each instance
+template <bool FOLD>
 __global__ __launch_bounds__(kThreads, 1) void decode_step_persistent(DArgs a) {
+  a.fold = FOLD;
   __shared__ __attribute__((aligned(16))) Shared s;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -867,9 +871,14 @@ hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream) {
   int cus = 0;
   if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
   int per_cu = 0;
-  if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_persistent, kThreads, 0)) !=
+  if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_persistent<true>, kThreads, 0)) !=
       hipSuccess)
     return e;
+  int per_cu2 = 0;
+  if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, decode_step_persistent<false>, kThreads, 0)) !=
+      hipSuccess)
+    return e;
+  per_cu = std::min(per_cu, per_cu2);
   if (per_cu < 1 || cus < 1) return hipErrorNotSupported;
   // At most one workgroup per CU, and no more than H or I: then every
   // workgroup owns rows in every phase, so every phase's output needs every
@@ -922,7 +931,10 @@ hipError_t launch_decode_step(const DecodeProblem& p, hipStream_t stream) {
   // running.  Should some not be (another stream's kernel holding CUs), the
   // resident ones wait for them with bounded waits, so the launch ends with
   // the error word set rather than hanging.
-  hipLaunchKernelGGL(decode_step_persistent, dim3(G), dim3(kThreads), 0, stream, a);
+  if (a.fold)
+    hipLaunchKernelGGL(decode_step_persistent<true>, dim3(G), dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_step_persistent<false>, dim3(G), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
