@@ -128,7 +128,7 @@ int gemm_pick_tile(const GemmProblem& p) {
       {TILE_256x256_W8, 256, 256, 1, 1.00f}, {TILE_256x128_W8, 256, 128, 1, 0.85f},
       {TILE_128x256, 128, 256, 1, 0.80f},    {TILE_128x128_W8, 128, 128, 2, 0.90f},
       {TILE_64x128, 64, 128, 3, 0.50f},      {TILE_128x64, 128, 64, 3, 0.50f},
-      {TILE_64x64, 64, 64, 4, 0.52f},
+      {TILE_64x64, 64, 64, 4, 0.52f},        {TILE_128x192_W8, 128, 192, 1, 0.80f},
   };
   const int cus = 256;
   int best = TILE_64x64;
@@ -136,6 +136,11 @@ int gemm_pick_tile(const GemmProblem& p) {
   const bool i8 = p.dtype == DT_W8A16;
   for (const Cand& c : cands) {
     if (c.bn == 64 && p.epilogue == EPI_SILU_MUL) continue;
+    // 128x192: k-contiguous fp16 / bf16 weights, one round of tiles (where
+    // it was measured: TinyLlama gate/up, ViT-B/16 fc1)
+    if (c.id == TILE_128x192_W8 && (p.dtype == DT_W8A16 || !p.b_nt ||
+                                    ((p.M + 127) / 128) * ((p.N + 191) / 192) * p.batch > cus))
+      continue;
     // int8 B converts every weight once per tile row: tall tiles amortise
     // it, and the latency-bound small shapes want the most workgroups
     // (measured on the Qwen2.5-0.5B int8 shapes at M = 256)
@@ -183,7 +188,9 @@ int tile_for(const GemmProblem& p) {
     return t128 >= 256 ? TILE_128x128 : TILE_64x64;
   }
   int tile = p.tile >= 0 ? p.tile : knob_or(KNOB_GEMM_TILE, -1);
-  if (tile < 0 || tile >= TILE_COUNT) tile = gemm_pick_tile(p);
+  // (an override of 128x192 for a layout it does not take: the picker's tile)
+  if (tile < 0 || tile >= TILE_COUNT || (tile == TILE_128x192_W8 && (!p.b_nt || p.dtype == DT_W8A16)))
+    tile = gemm_pick_tile(p);
   if (p.epilogue == EPI_SILU_MUL && kTiles[tile].BN < 128) tile = TILE_64x128;
   return tile;
 }

@@ -887,6 +887,15 @@ struct TileShape {
 // TinyLlama gate/up with SiLU-mul on the 8-wave 256x128 tile went 33.7 ->
 // 30.7 us (the 8-wave 128x128 tile at two per CU: 33.1 us; with three or
 // four stages, one per CU, 40.8 / 42.0 us).
+// The 8-wave 128x192 tile (three 32-column MFMA blocks a wave, 40 KB a
+// stage, one workgroup per CU) fills more CUs in one round where 128-row
+// tiles would need two per CU: TinyLlama gate/up (512 x 11264) runs 236
+// tiles on 236 CUs instead of 176 of 256x128, 28.4 -> 27.6 us and the block
+// 76.6 -> 74.9-75.4 us; ViT-B/16 fc1 (1576 x 3072) 208 tiles instead of 312
+// of 128x128 at two per CU, 17.3 -> 15.8 us.  Four waves of 64x96 on the same
+// tile: 29.4 and 18.1 us.  It takes k-contiguous B ([N, K]) only: an NN
+// B row of 192 columns (384 bytes) does not divide the 1 KB wave load, and
+// 192 rows do not split into the int8 B loads' 16-row groups over 8 waves.
 constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 256, 128, 128, 64, 2},  // TILE_256x256
     {128, 256, 64, 128, 64, 3, false, 0, 3},   // TILE_128x256
@@ -902,6 +911,7 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 256, 128, 64, 32, 3, true},  // TILE_256x256_PP
     {256, 128, 64, 64, 64, 3},         // TILE_256x128_W8
     {128, 128, 32, 64, 64, 2, false, 0, 3},    // TILE_128x128_W8
+    {128, 192, 32, 96, 64, 3, false, 0, 3},    // TILE_128x192_W8
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false, bool RAGGED = false>
@@ -936,6 +946,9 @@ hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
     case TILE_256x256_PP: return launch_one<TILE_256x256_PP, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     case TILE_256x128_W8: return launch_one<TILE_256x128_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     case TILE_128x128_W8: return launch_one<TILE_128x128_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_128x192_W8:
+      if constexpr (BI8 || NN) return hipErrorNotSupported;  // (k-contiguous fp16 / bf16 B only)
+      else return launch_one<TILE_128x192_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
   }
 }

@@ -9,7 +9,13 @@ from oracle import hot_path as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = list(range(14))  # every instantiated tile shape (TileId)
+TILES = list(range(15))  # every instantiated tile shape (TileId)
+NT_ONLY = {14}  # 128x192 takes k-contiguous B only (a forced override of it in NN runs the picker's tile)
+
+
+def skip_nn(tile, layout):
+    if layout == "nn" and tile in NT_ONLY:
+        pytest.skip("128x192 tile: k-contiguous B only")
 
 
 def run_gemm(pkg, dev, a, b, layout, **kw):
@@ -30,6 +36,7 @@ def test_config1_gemm_1024_nn(pkg, dev, seed_a, seed_b):
 @pytest.mark.parametrize("layout", ["nn", "nt"])
 @pytest.mark.parametrize("tile", TILES)
 def test_gemm_exact_integer_every_tile(pkg, dev, force_tile, layout, tile):
+    skip_nn(tile, layout)
     d = np.load(GOLDEN / f"gemm_int_{layout}.npz")
     force_tile(tile)
     a = torch.from_numpy(d["a"]).half()
@@ -308,6 +315,7 @@ def test_gemm_split_k_epilogues(pkg, dev, force_splits, epi):
 def test_gemm_split_k_every_tile_exact(pkg, dev, force_tile, force_splits, tile, layout):
     # integer-valued operands: every partial tile and their fp32 sum are
     # exact, so the fixed-up output must equal the rounded exact product
+    skip_nn(tile, layout)
     force_tile(tile)
     force_splits(3)
     M, N, K = 300, 264, 2112
@@ -415,7 +423,9 @@ def test_gemm_split_k_default_down_projection(pkg, dev):
 @pytest.mark.parametrize("tile", TILES)
 def test_gemm_f32_out_every_tile(pkg, dev, force_tile, tile):
     # fp32 output straight from the accumulators (HexKL's f16 x f16 -> f32
-    # matmul): integer operands, so every tile's result is exact
+    # matmul, w [n_inner, n_col]: NN): integer operands, so every tile's
+    # result is exact
+    skip_nn(tile, "nn")
     force_tile(tile)
     g = torch.Generator().manual_seed(44)
     act = torch.randint(-3, 4, (300, 200), generator=g).half()
