@@ -194,7 +194,7 @@ def test_gemm_bias_n_not_a_multiple_of_8(pkg, dev, force_tile, epi, tile):
     assert (c[:, N:] == 7.0).all()
 
 
-@pytest.mark.parametrize("tile", [None, 0, 1, 2, 3, 4, 11, 12, 13])
+@pytest.mark.parametrize("tile", [None, 0, 1, 2, 3, 4, 11, 12, 13, 14])
 def test_gemm_silu_mul(pkg, dev, force_tile, tile):
     force_tile(tile)
     M, I, K = 200, 320, 256
@@ -206,6 +206,34 @@ def test_gemm_silu_mul(pkg, dev, force_tile, tile):
     torch.cuda.synchronize()
     exp = ref.silu_mul_linear(x.numpy(), wg.numpy(), wu.numpy())
     assert ref.max_rel_err(np32(h.cpu()), exp) <= TOL
+
+
+@pytest.mark.parametrize("epi", [None, "bias_gelu_tanh", "silu_mul"])
+def test_gemm_bf16_tile_128x192(pkg, dev, force_tile, epi):
+    # the 8-wave 128x192 tile on bf16 operands, with a ragged last tile
+    # column (N = 416: 32 of its 192 columns) and the epilogues it runs in
+    # the ViT MLP and the LLaMA gate/up projection
+    force_tile(14)
+    M, N, K = 200, 416, 320
+    a = normal((M, K), 45, dtype=torch.bfloat16)
+    w = normal((N, K), 46, 0.05, dtype=torch.bfloat16)
+    bias = normal((N,), 47, 0.5, dtype=torch.bfloat16) if epi == "bias_gelu_tanh" else None
+    y = pkg.linear(a.to(dev), w.to(dev), None if bias is None else bias.to(dev),
+                   epilogue="gelu_tanh" if epi == "bias_gelu_tanh" else epi)
+    torch.cuda.synchronize()
+    # (silu_mul: w holds packed gate/up rows, which the oracle unpacks itself)
+    exp = ref.gemm_epilogue(np32(a), np32(w), "nt", epi, None if bias is None else np32(bias))
+    assert tuple(y.shape) == (M, N // 2 if epi == "silu_mul" else N)
+    assert ref.max_rel_err(np32(y.cpu()), exp) <= TOL
+
+
+def test_gemm_tile_128x192_override_nn_runs_picked_tile(pkg, dev, force_tile):
+    # 128x192 takes k-contiguous B only: forced on an NN GEMM, the picker's
+    # tile runs instead and the integer product stays exact
+    force_tile(14)
+    d = np.load(GOLDEN / "gemm_int_nn.npz")
+    c = run_gemm(pkg, dev, torch.from_numpy(d["a"]).half(), torch.from_numpy(d["b"]).half(), "nn")
+    assert np.array_equal(c.numpy(), f16_round(d["c"]))
 
 
 def test_gemm_alpha(pkg, dev):
