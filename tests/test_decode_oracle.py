@@ -1,4 +1,4 @@
-"""Pin oracle.decode_step, the checker of the persistent decode step.
+"""Pin oracle.decode_step, the oracle the persistent decode step is compared with.
 
 The step is the HF Qwen2 forward of one token at position 0
 (benchmark_models/run_qwen2.5-0.5b.py:171-173,224-233).  transformers'
