@@ -228,7 +228,7 @@ int hxmi_bgemm_bf16(const void* A, const void* B, void* C, const void* bias, int
 namespace {
 int gemv_common(int dtype, const char* name, const void* x, const void* W, const void* bias, void* y, int64_t M,
                 int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+                int64_t workspace_bytes, void* stream, int w_cached = 0) {
   REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", name);
   if (M == 0 || N == 0) return ok();
   REQUIRE(x && W && y, "%s: null pointer", name);
@@ -254,6 +254,7 @@ int gemv_common(int dtype, const char* name, const void* x, const void* W, const
   p.dtype = dtype;
   p.ws = workspace_bytes > 0 ? workspace : nullptr;
   p.ws_bytes = workspace_bytes > 0 ? workspace_bytes : 0;
+  p.w_cached = w_cached;
   return from_hip(hxmi::launch_gemv(p, (hipStream_t)stream), name);
 }
 }  // namespace
@@ -605,8 +606,12 @@ static int decode_common(const char* name, const void* x, const void* w_qkv, con
   const hipError_t e = hxmi::launch_decode_step(p, (hipStream_t)stream);
   if (e != hipSuccess) return from_hip(e, name);
   if (!w_lm) return ok();
+  // the lm_head after the non-temporal layer-weight stream: its own weight
+  // loads with the ordinary cache policy (Qwen2.5-0.5B folded forward
+  // 449.3-449.5 -> 447.7-448.2 us; the same loads were 3 us slower after a
+  // layer stream with the ordinary policy)
   return gemv_common(hxmi::DT_F16, name, h_out, w_lm, nullptr, logits, 1, vocab, hidden, hidden, hidden, vocab,
-                     nullptr, 0, stream);
+                     nullptr, 0, stream, 1);
 }
 
 int hxmi_decode_step_f16(const void* x, const void* w_qkv, const void* b_qkv, const void* w_o, const void* w_gu,

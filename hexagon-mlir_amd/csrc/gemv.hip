@@ -44,6 +44,7 @@ struct VArgs {
   // a tile resets its counter to zero, so every launch leaves them zero.
   int kg;
   char* ws;
+  int w_cached;  // GemvProblem::w_cached
 };
 
 typedef float float2v __attribute__((ext_vector_type(2)));
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma(VArgs a) {
 // stays a few percent of the MFMA units at HBM speed.
 // (launched for fp16 weights; int8 weights run gemv_pair_i8 below, which
 // keeps this layout and overlaps the first tile's loads with x's staging)
-template <typename T, bool I8, int NWIN, int U, int YKEEP>
+template <typename T, bool I8, int NWIN, int U, int YKEEP, bool WNT = true>
 __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
   constexpr int KW = I8 ? 128 : 64;   // k per 128-byte window
   constexpr int FPW = I8 ? 4 : 2;     // x fragments per window
@@ -307,7 +308,8 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
       for (int u = 0; u < U; ++u) {
         const int j = j0 + u;
         const bool ok = j < NWIN && rowok && (KW * j + CK * chunk) < a.K;
-        wv[u] = load16_nt(rW, ok ? wrow + (uint32_t)(j * 128) : kOOB);
+        const uint32_t off = ok ? wrow + (uint32_t)(j * 128) : kOOB;
+        wv[u] = WNT ? load16_nt(rW, off) : load16(rW, off);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -618,6 +620,8 @@ hipError_t launch_pair(const VArgs& v, hipStream_t stream) {
   }
   else if (v.M > 4)
     hipLaunchKernelGGL((gemv_pair<T, false, 16, 16, 6>), dim3(blocks), dim3(256), 0, stream, v);
+  else if (v.w_cached)
+    hipLaunchKernelGGL((gemv_pair<T, false, 16, 16, 0, false>), dim3(blocks), dim3(256), 0, stream, v);
   else
     hipLaunchKernelGGL((gemv_pair<T, false, 16, 16, 0>), dim3(blocks), dim3(256), 0, stream, v);
   return hipGetLastError();
@@ -891,6 +895,7 @@ hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
   v.ldy = p.ldy;
   v.kg = 1;
   v.ws = nullptr;
+  v.w_cached = p.w_cached;
   const GemvPlan g = gemv_plan(p);
   const bool bf = p.dtype == DT_BF16;  // bf16 x, W, bias, y (fp16 weights otherwise; int8 takes fp16 x)
   if (g.valu)

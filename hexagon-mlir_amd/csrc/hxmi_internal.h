@@ -131,6 +131,10 @@ struct GemvProblem {
   int64_t ldx, ldw, ldy;
   int w_int8;
   int dtype = DT_F16;  // DT_F16 or DT_BF16 (int8 weights: fp16 activations)
+  // 1: the whole-line fp16 / bf16 kernel loads W with the ordinary cache
+  // policy instead of non-temporal (the decode forward's lm_head, which runs
+  // after a non-temporal stream of the layer weights)
+  int w_cached = 0;
   void* ws;  // optional workspace for K split over workgroups
   int64_t ws_bytes;
 };
