@@ -102,7 +102,9 @@ struct AttnShape {
   static constexpr bool ok = NT <= 1024 && (KS - 1) * QG * NV * 64 * 4 <= 2 * CHUNK;
 };
 
-template <int D, int QG, int KS, bool MASK>
+// PIPE: the key blocks of a chunk start load index by load index (below);
+// chosen at launch for sequences of at least one chunk.
+template <int D, int QG, int KS, bool MASK, bool PIPE>
 __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
   using Sh = AttnShape<D, QG, KS>;
   static_assert(Sh::ok, "attention shape");
@@ -184,27 +186,41 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
       load_lds16(rV, (HXMI_LDS void*)to_lds(vs + (i * NW + w) * 1024), vo);
     }
   };
-  // The first chunk's K / V loads go out before the Q loads: the compiler
-  // waits for Q (which the chunk loop reads) before entering the loop, so
-  // Q issued first would put a whole memory round trip ahead of the K / V
-  // requests instead of the two overlapping.
-  if (kend > 0) issue_chunk(0);
-  // Q fragments of this wave's 32 queries (zero past the sequence)
+  // Q fragments of this wave's 32 queries (zero past the sequence), then
+  // the first chunk's K / V: the chunk's loads are waited for load index by
+  // load index (below), which leaves the later ones in flight only when Q
+  // was issued before them.  The Q loads take no branch (an offset past the
+  // buffer reads zeros), so the compiler does not wait for them early.
   short8v qf[DS];
+  {
+    const __amdgpu_buffer_rsrc_t rQ = make_rsrc(Q, 0x7fffffffu);
 #pragma unroll
-  for (int s = 0; s < DS; ++s) {
-    qf[s] = short8v{};
-    if (qme < a.sq) qf[s] = *(const short8v*)(Q + ((int64_t)qme * a.ldq + s * 16 + h * 8) * 2);
+    for (int s = 0; s < DS; ++s)
+      qf[s] = __builtin_bit_cast(
+          short8v, load16(rQ, qme < a.sq ? (uint32_t)(((int64_t)qme * a.ldq + s * 16 + h * 8) * 2) : kOOB));
   }
+  if (kend > 0) issue_chunk(0);
 
-  for (int c0 = 0; c0 < kend; c0 += KC) {
-    if (c0 > 0) {
-      __syncthreads();  // previous chunk fully consumed
-      issue_chunk(c0);
-    }
-    wait_vmcnt0();
-    __syncthreads();
-
+  // Keys [c0, c0 + KC) of one chunk, its loads issued: load index i of every
+  // wave brings keys [i KPL, (i + 1) KPL) of K and V.  PIPE: before the key
+  // blocks of round j (block kh + j KS of wave kh) every wave waits for its
+  // loads up to the last index the round reads (the next round's K for the
+  // scores computed ahead), then one barrier, so the first blocks start when
+  // their keys have landed rather than the whole chunk.  That pays on full
+  // chunks (2 x 12 x 1024: 17.2 -> 16.85 us; head dim 128, 16 x 512 causal:
+  // 10.47 -> 10.15 us) but not on a short one, where the extra barriers
+  // cost more than the overlap gives (ViT-B/16, 197 keys: 7.47 -> 7.56 us),
+  // so the launch takes PIPE only for sequences of at least KC keys; the
+  // other instance waits for a whole chunk once.  (One kernel with both
+  // paths, chosen per chunk, took 30-60 more VGPRs, and the head-dim-128
+  // instances then held one wave per SIMD instead of two.)
+  constexpr int KPL = NW * (1024 / RB);
+  constexpr int JMAX = KC / 32 / KS;
+  constexpr auto li_end = [](int b) constexpr {
+    const int i = ((b + 1) * 32 - 1) / KPL;  // the load index of block b's last key, within the chunk
+    return i < LPW - 1 ? i : LPW - 1;
+  };
+  auto run_chunk = [&](int c0) {
     const int cn = min(KC, wkend - c0);
     const int nblk = cn > 0 ? (cn + 31) >> 5 : 0;
     // S block b: D[key][query], lane holds query lane%32, keys 8g + 4h + j
@@ -302,18 +318,39 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
         }
       }
     };
+    constexpr bool pipe = PIPE;
+    constexpr int L0 = pipe ? li_end(KS - 1) : LPW - 1;
+    wait_vmcnt<2 * (LPW - 1 - L0)>();
+    barrier_after_lds_loads();
     float16v s_next = kh < nblk ? scores(kh) : float16v{};
     _Float16 mk_next[16];
     if (MASK && kh < nblk) mask_vals(kh, mk_next);
-    for (int b = kh; b < nblk; b += KS) {
-      float16v s = s_next;
-      _Float16 mk[16];
-      if constexpr (MASK) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mk[i] = mk_next[i];
+    static_for<JMAX>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      constexpr int need = li_end(KS - 1 + (j + 1) * KS), prev = li_end(KS - 1 + j * KS);
+      if constexpr (pipe && need > prev) {
+        wait_vmcnt<2 * (LPW - 1 - need)>();
+        barrier_after_lds_loads();
       }
-      block(b, s, s_next, mk, mk_next);
-    }
+      const int b = kh + j * KS;
+      if (b < nblk) {
+        float16v s = s_next;
+        _Float16 mk[16];
+        if constexpr (MASK) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mk[i] = mk_next[i];
+        }
+        block(b, s, s_next, mk, mk_next);
+      }
+    });
+  };
+  // the first chunk outside the loop: the compiler waits for every
+  // outstanding load before a loop that reads registers loaded before it (Q)
+  if (kend > 0) run_chunk(0);
+  for (int c0 = KC; c0 < kend; c0 += KC) {
+    __syncthreads();  // previous chunk fully consumed
+    issue_chunk(c0);
+    run_chunk(c0);
   }
 
   // merge the key-split partials of each query group into wave kh = 0
@@ -373,11 +410,16 @@ hipError_t launch_cfg(AArgs a, const AttnProblem& p, bool mask, hipStream_t stre
     a.nqb = (int)((p.s + 32 * QG - 1) / (32 * QG));
     const int64_t blocks = p.bh * a.nqb;
     if (blocks >= (1ll << 31)) return hipErrorInvalidValue;
-    if (mask)
-      hipLaunchKernelGGL((attention_fwd<D, QG, KS, true>), dim3((unsigned)blocks), dim3(64 * QG * KS), 0, stream, a);
+    const dim3 grid((unsigned)blocks), block(64 * QG * KS);
+    const bool pipe = p.skv >= AttnShape<D, QG, KS>::KC;
+    if (mask && pipe)
+      hipLaunchKernelGGL((attention_fwd<D, QG, KS, true, true>), grid, block, 0, stream, a);
+    else if (mask)
+      hipLaunchKernelGGL((attention_fwd<D, QG, KS, true, false>), grid, block, 0, stream, a);
+    else if (pipe)
+      hipLaunchKernelGGL((attention_fwd<D, QG, KS, false, true>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL((attention_fwd<D, QG, KS, false>), dim3((unsigned)blocks), dim3(64 * QG * KS), 0, stream,
-                         a);
+      hipLaunchKernelGGL((attention_fwd<D, QG, KS, false, false>), grid, block, 0, stream, a);
     return hipGetLastError();
   }
 }

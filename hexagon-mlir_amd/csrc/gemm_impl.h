@@ -114,13 +114,6 @@ __device__ __forceinline__ short8v read_kc(const char* tile, int r_off, int s, i
   return *(const short8v*)(tile + r * RB + ((c ^ kc_swz<RB>(r)) << 4));
 }
 
-// vmcnt(n) with the other counters left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 template <int BN>
 __device__ __forceinline__ int nn_swz(int k) {
   return (BN / 8 >= 16) ? ((k & 3) << 2) : ((k & 3) << 1);
@@ -208,17 +201,6 @@ __device__ __forceinline__ short8v keep_first(short8v v, int n) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = e < n ? v[e] : (short)0;
   return v;
-}
-
-template <typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order.
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // Instruction order inside one substep region (the compiler's scheduler
