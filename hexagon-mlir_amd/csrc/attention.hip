@@ -211,7 +211,8 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
   // 10.47 -> 10.15 us) but not on a short one, where the extra barriers
   // cost more than the overlap gives (ViT-B/16, 197 keys: 7.47 -> 7.56 us),
   // so the launch takes PIPE only for sequences of at least KC keys; the
-  // other instance waits for a whole chunk once.  (One kernel with both
+  // other instance waits for the first half of the chunk, then for the
+  // rest (ViT-B/16 7.35-7.41 -> 7.31-7.32 us against one wait for all).  (One kernel with both
   // paths, chosen per chunk, took 30-60 more VGPRs, and the head-dim-128
   // instances then held one wave per SIMD instead of two.)
   constexpr int KPL = NW * (1024 / RB);
@@ -319,7 +320,8 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
       }
     };
     constexpr bool pipe = PIPE;
-    constexpr int L0 = pipe ? li_end(KS - 1) : LPW - 1;
+    // (the other instance: the first half of the chunk, then the rest)
+    constexpr int L0 = pipe ? li_end(KS - 1) : (li_end(KS - 1) > LPW / 2 - 1 ? li_end(KS - 1) : LPW / 2 - 1);
     wait_vmcnt<2 * (LPW - 1 - L0)>();
     barrier_after_lds_loads();
     float16v s_next = kh < nblk ? scores(kh) : float16v{};
@@ -328,8 +330,10 @@ __global__ __launch_bounds__(64 * QG * KS) void attention_fwd(AArgs a) {
     static_for<JMAX>([&](auto J) {
       constexpr int j = decltype(J)::value;
       constexpr int need = li_end(KS - 1 + (j + 1) * KS), prev = li_end(KS - 1 + j * KS);
-      if constexpr (pipe && need > prev) {
-        wait_vmcnt<2 * (LPW - 1 - need)>();
+      constexpr int wn = pipe ? need : (need <= L0 ? L0 : LPW - 1);
+      constexpr int wp = pipe ? prev : (prev <= L0 ? L0 : LPW - 1);
+      if constexpr (wn > wp) {
+        wait_vmcnt<2 * (LPW - 1 - wn)>();
         barrier_after_lds_loads();
       }
       const int b = kh + j * KS;
