@@ -894,6 +894,7 @@ constexpr TileShape kTiles[TILE_COUNT] = {
     {256, 128, 64, 64, 64, 3},         // TILE_256x128_W8
     {128, 128, 32, 64, 64, 2, false, 0, 3},    // TILE_128x128_W8
     {128, 192, 32, 96, 64, 3, false, 0, 3},    // TILE_128x192_W8
+    {64, 64, 32, 32, 64, 4, false, 0, 3},      // TILE_64x64_S4
 };
 
 template <int TILE, bool NN, typename T, int EPI, bool OUTF32, bool BI8, bool RMS = false, bool RAGGED = false>
@@ -931,6 +932,7 @@ hipError_t launch_tile(int tile, const KArgs& k, hipStream_t stream) {
     case TILE_128x192_W8:
       if constexpr (BI8 || NN) return hipErrorNotSupported;  // (k-contiguous fp16 / bf16 B only)
       else return launch_one<TILE_128x192_W8, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
+    case TILE_64x64_S4: return launch_one<TILE_64x64_S4, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
     default: return launch_one<TILE_64x64, NN, T, EPI, OUTF32, BI8, RMS>(k, stream);
   }
 }

@@ -113,6 +113,7 @@ enum TileId {
   TILE_256x128_W8,  // 8 waves of 64x64, 3 stages
   TILE_128x128_W8,  // 8 waves of 32x64
   TILE_128x192_W8,  // 8 waves of 32x96, 3 stages; k-contiguous fp16 / bf16 B only (not NN, not int8)
+  TILE_64x64_S4,    // TILE_64x64 with 4 LDS stages
   TILE_COUNT
 };
 

@@ -9,7 +9,7 @@ from oracle import hot_path as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = list(range(15))  # every instantiated tile shape (TileId)
+TILES = list(range(16))  # every instantiated tile shape (TileId)
 NT_ONLY = {14}  # 128x192 takes k-contiguous B only (a forced override of it in NN runs the picker's tile)
 
 

@@ -19,7 +19,7 @@ from oracle import hot_path as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = list(range(15))  # every GEMM tile shape (TileId)
+TILES = list(range(16))  # every GEMM tile shape (TileId)
 
 
 def check(y, x, wf_cpu, exp_hf, eps, epi=None):
