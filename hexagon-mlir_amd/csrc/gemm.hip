@@ -179,7 +179,7 @@ int gemm_pick_tile(const GemmProblem& p) {
   // 64x64 tiles over K >= 2048: a fourth LDS stage (two workgroups still fit
   // a CU).  The 512-token O projection in the TinyLlama block sequence,
   // weights from HBM: block 75.46-75.90 -> 74.75-75.04 us (72.8-73.3 against
-  // 74.3-74.6 on another box); the 1024^3 GEMM, its operands in L2, ran
+  // 74.3-74.6 on another MI355X); the 1024^3 GEMM, its operands in L2, ran
   // 6.42 -> 6.53 us with it and keeps three stages
   if (best == TILE_64x64 && !i8 && p.K >= 2048) best = TILE_64x64_S4;
   return best;

@@ -352,7 +352,7 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
 // staged: x's fragments are loaded into registers first and the first
 // tile's weights right after, so the wait before storing x to LDS covers
 // the x loads only and the weights' round trip overlaps the staging (int8
-// lm_head at M = 16 29.0 -> 27.1 us on one box).  Scale and bias are one
+// lm_head at M = 16 29.0 -> 27.1 us on one MI355X).  Scale and bias are one
 // 32-bit buffer load each per lane (rows n, n + 1; n is even, N % 4 == 0),
 // out of range or absent reading as zero, kept as raw bits until the
 // epilogue, so no branch makes the compiler drain the loads in flight.  The
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(256) void gemv_pair(VArgs a) {
 // round; their y meets in LDS and leaves as 64-byte row pieces (16-byte
 // stores from one wave) instead of 4-byte stores from every lane.  At M = 16
 // the scattered stores cost ~3 us of the lm_head's 25 (a timing copy
-// without y stores ran 22.6 us); staged, paired runs on two boxes gained
+// without y stores ran 22.6 us); staged, paired runs on two MI355Xs gained
 // 0.25-0.5 us (25.45 -> 24.98, 25.66 -> 25.42).  Rounds of eight
 // tiles (two per wave, 128-byte pieces) ran 27.8 us: twice the weight
 // streams in flight per wave, as with more workgroups.
